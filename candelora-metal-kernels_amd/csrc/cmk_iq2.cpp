@@ -1,0 +1,432 @@
+// cmk_iq2.cpp — implementation of the C ABI declared in include/cmk_iq2.h.
+//
+// Host-side dispatch for the IQ2_XXS path: argument validation with the
+// reference's error texts (src/iq2_matmul.rs:210-311, 367-433, 559-591), kernel
+// selection by shape, and thin HIP runtime wrappers.  Nothing here allocates
+// device memory on a launch path.
+#include "cmk_iq2.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cinttypes>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+
+#include "iq2xxs_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return CMK_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(CMK_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+const char* variant_name(int v) {
+  switch (v) {
+    case CMK_IQ2_XXS: return "Iq2Xxs";
+    case CMK_IQ2_XS: return "Iq2Xs";
+    case CMK_IQ2_S: return "Iq2S";
+    case CMK_IQ3_S: return "Iq3S";
+    default: return "Unknown";
+  }
+}
+
+// Largest m served by the GEMV family when x is f16/bf16 (above it: MFMA GEMM).
+constexpr size_t kGemvMaxM = 16;
+constexpr size_t kWorkspaceAlign = 256;
+
+bool checked_mul(size_t a, size_t b, size_t* out) {
+  if (a != 0 && b > SIZE_MAX / a) return false;
+  *out = a * b;
+  return true;
+}
+
+struct Dims {
+  uint32_t m, out_dim, in_dim, bpr;
+};
+
+// Per-device CU counts, read once.
+std::mutex g_dev_mu;
+int g_cu_count[64] = {0};
+
+int current_cu_count(int* cus) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= 64) return fail(CMK_ERR_NO_DEVICE, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  if (g_cu_count[dev] == 0) {
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+    g_cu_count[dev] = n > 0 ? n : 1;
+  }
+  *cus = g_cu_count[dev];
+  return CMK_OK;
+}
+
+// Path decision shared by the launch, the workspace query and the path query.
+enum class Path { Gemv, Gemm, Simple };
+
+Path choose_path(int x_dtype, size_t m, uint32_t in_dim, bool wb_aligned16, bool ws_aligned2) {
+  const bool half_x = x_dtype == CMK_F16 || x_dtype == CMK_BF16;
+  if (half_x && m > kGemvMaxM && ws_aligned2) return Path::Gemm;
+  if (cmk::gemv_supported(in_dim) && wb_aligned16 && ws_aligned2) return Path::Gemv;
+  return Path::Simple;
+}
+
+size_t workspace_for(Path p, bool w8a8, size_t m) {
+  if (!w8a8 || p == Path::Gemv) return 0;
+  return ((m * sizeof(float) + kWorkspaceAlign - 1) / kWorkspaceAlign) * kWorkspaceAlign;
+}
+
+// Shared validation of cmk_iq2_matmul / cmk_iq2_matmul_workspace_size.
+// Resolves the activation mode (W4A8 non-strict runs as OFF).
+int validate_matmul(int x_dtype, size_t m, size_t out_dim, size_t in_dim, int variant, int* mode,
+                    int strict, size_t wb_len, size_t ws_len, bool check_sizes, Dims* dims) {
+  // iq2_matmul_with_activation_quant (src/iq2_matmul.rs:559-591)
+  if (*mode == CMK_ACT_QUANT_W4A8) {
+    if (strict)
+      return fail(CMK_ERR_UNSUPPORTED,
+                  "activation quant mode W4A8 requested in strict mode, but W4A8 kernel path is "
+                  "not implemented yet");
+    *mode = CMK_ACT_QUANT_OFF;
+  }
+  if (*mode != CMK_ACT_QUANT_OFF && *mode != CMK_ACT_QUANT_W8A8)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "invalid activation quant mode: %d", *mode);
+  // iq2_matmul_metal guards (src/iq2_matmul.rs:210-311)
+  if (out_dim == 0 || in_dim == 0)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul expects non-zero dimensions");
+  if (variant != CMK_IQ2_XXS) {
+    if (variant < CMK_IQ2_XXS || variant > CMK_IQ3_S)
+      return fail(CMK_ERR_INVALID_ARGUMENT, "invalid iq2 variant: %d", variant);
+    return fail(CMK_ERR_UNSUPPORTED,
+                "iq2_matmul variant %s is not implemented by the ROCm backend (Iq2Xxs only)",
+                variant_name(variant));
+  }
+  if (x_dtype != CMK_F32 && x_dtype != CMK_F16 && x_dtype != CMK_BF16)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                *mode == CMK_ACT_QUANT_W8A8 ? "iq2_matmul_w8a8 unsupported x dtype: %d"
+                                            : "iq2_matmul unsupported x dtype: %d",
+                x_dtype);
+  const size_t bpr = (in_dim + 255) / 256;
+  size_t blocks, expected_bytes, expected_scales;
+  if (!checked_mul(out_dim, bpr, &blocks) || !checked_mul(blocks, 64, &expected_bytes))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul bytes size overflow");
+  if (!checked_mul(blocks, 2, &expected_scales))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul scales size overflow");
+  if (check_sizes) {
+    if (wb_len < expected_bytes)
+      return fail(CMK_ERR_INVALID_ARGUMENT,
+                  "iq2_matmul weight_bytes too small: got %zu expected at least %zu", wb_len,
+                  expected_bytes);
+    if (ws_len < expected_scales)
+      return fail(CMK_ERR_INVALID_ARGUMENT,
+                  "iq2_matmul weight_scales too small: got %zu expected at least %zu", ws_len,
+                  expected_scales);
+  }
+  size_t total;
+  if (!checked_mul(m, out_dim, &total))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul output size overflow");
+  if (m > UINT32_MAX) return fail(CMK_ERR_INVALID_ARGUMENT, "m too large");
+  if (out_dim > UINT32_MAX) return fail(CMK_ERR_INVALID_ARGUMENT, "out_dim too large");
+  if (in_dim > UINT32_MAX) return fail(CMK_ERR_INVALID_ARGUMENT, "in_dim too large");
+  if (bpr > UINT32_MAX) return fail(CMK_ERR_INVALID_ARGUMENT, "blocks_per_row too large");
+  dims->m = (uint32_t)m;
+  dims->out_dim = (uint32_t)out_dim;
+  dims->in_dim = (uint32_t)in_dim;
+  dims->bpr = (uint32_t)bpr;
+  return CMK_OK;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* cmk_last_error(void) { return g_last_error.c_str(); }
+
+int cmk_abi_version(void) { return CMK_IQ2_ABI_VERSION; }
+
+int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, size_t in_dim,
+                                  cmk_iq2_variant variant, cmk_act_quant_mode mode,
+                                  size_t* bytes) {
+  if (!bytes) return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul null pointer argument");
+  int md = (int)mode;
+  Dims dims;
+  int rc = validate_matmul((int)x_dtype, m, out_dim, in_dim, (int)variant, &md, 0, 0, 0, false,
+                           &dims);
+  if (rc != CMK_OK) return rc;
+  // Assume allocator-aligned buffers (hipMalloc gives 256-byte alignment).
+  Path p = choose_path((int)x_dtype, m, dims.in_dim, true, true);
+  // The simple path can still be chosen at launch for unaligned weights; report
+  // the larger need so either choice is covered.
+  size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, m);
+  size_t need_simple = workspace_for(Path::Simple, md == CMK_ACT_QUANT_W8A8, m);
+  *bytes = need > need_simple ? need : need_simple;
+  return ok();
+}
+
+int cmk_iq2_matmul_path(cmk_dtype x_dtype, size_t m, size_t out_dim, size_t in_dim,
+                        cmk_act_quant_mode mode) {
+  (void)out_dim;
+  (void)mode;
+  return choose_path((int)x_dtype, m, (uint32_t)(in_dim > UINT32_MAX ? UINT32_MAX : in_dim), true,
+                     true) == Path::Gemm
+             ? 1
+             : 0;
+}
+
+int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
+                   const uint8_t* weight_bytes, size_t weight_bytes_len,
+                   const uint8_t* weight_scales, size_t weight_scales_len, size_t out_dim,
+                   size_t in_dim, cmk_iq2_variant variant, cmk_act_quant_mode mode, int strict,
+                   float* out, void* workspace, size_t workspace_bytes, void* stream) {
+  int md = (int)mode;
+  Dims dims;
+  int rc = validate_matmul((int)x_dtype, m, out_dim, in_dim, (int)variant, &md, strict,
+                           weight_bytes_len, weight_scales_len, true, &dims);
+  if (rc != CMK_OK) return rc;
+  if (m == 0) return ok();  // empty activation: nothing to compute (src/iq2_matmul.rs:265-267)
+  size_t need_x;
+  if (!checked_mul(m, in_dim, &need_x))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul x size overflow");
+  if (x_len < need_x)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul x too small: got %zu expected at least %zu",
+                x_len, need_x);
+  if (!x || !weight_bytes || !weight_scales || !out)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul null pointer argument");
+  const size_t esize = x_dtype == CMK_F32 ? 4 : 2;
+  if (!aligned(x, esize))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul x must be aligned to its element size");
+  if (!aligned(out, 4))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul out must be 4-byte aligned");
+
+  const bool w8a8 = md == CMK_ACT_QUANT_W8A8;
+  Path p = choose_path((int)x_dtype, m, dims.in_dim, aligned(weight_bytes, 16),
+                       aligned(weight_scales, 2));
+  if (p == Path::Gemm && !aligned(weight_bytes, 8)) p = Path::Simple;
+  const size_t need_ws = workspace_for(p, w8a8, m);
+  if (need_ws > 0 && (workspace == nullptr || workspace_bytes < need_ws))
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "iq2_matmul workspace too small: got %zu expected at least %zu (see "
+                "cmk_iq2_matmul_workspace_size)",
+                workspace ? workspace_bytes : (size_t)0, need_ws);
+  if (need_ws > 0 && !aligned(workspace, 4))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul workspace must be 4-byte aligned");
+
+  int cus = 0;
+  rc = current_cu_count(&cus);
+  if (rc != CMK_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipSuccess;
+  float* row_inv = need_ws > 0 ? static_cast<float*>(workspace) : nullptr;
+  if (row_inv) {
+    e = cmk::launch_iq2xxs_row_inv_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s);
+    if (e != hipSuccess) return hip_fail(e, "iq2_matmul row scale launch");
+  }
+  switch (p) {
+    case Path::Gemv:
+      e = cmk::launch_iq2xxs_gemv(x, (int)x_dtype, dims.m, weight_bytes, weight_scales, out,
+                                  dims.out_dim, dims.in_dim, w8a8, cus, s);
+      break;
+    case Path::Gemm:
+      e = cmk::launch_iq2xxs_gemm(x, (int)x_dtype, dims.m, weight_bytes, weight_scales, out,
+                                  dims.out_dim, dims.in_dim, row_inv, s);
+      break;
+    case Path::Simple:
+      e = cmk::launch_iq2xxs_matmul_simple(x, (int)x_dtype, dims.m, weight_bytes, weight_scales,
+                                           out, dims.out_dim, dims.in_dim, row_inv, cus, s);
+      break;
+  }
+  if (e != hipSuccess) return hip_fail(e, "iq2_matmul launch");
+  return ok();
+}
+
+int cmk_iq2_dequantize(const uint8_t* weight_bytes, size_t weight_bytes_len,
+                       const uint8_t* weight_scales, size_t weight_scales_len, size_t out_dim,
+                       size_t in_dim, cmk_iq2_variant variant, cmk_dtype out_dtype, void* out,
+                       void* stream) {
+  // iq2_dequantize_to_f16_metal guards (src/iq2_matmul.rs:367-433)
+  if (out_dim == 0 || in_dim == 0)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 expects non-zero dimensions");
+  if (variant != CMK_IQ2_XXS) {
+    if ((int)variant < CMK_IQ2_XXS || (int)variant > CMK_IQ3_S)
+      return fail(CMK_ERR_INVALID_ARGUMENT, "invalid iq2 variant: %d", (int)variant);
+    return fail(CMK_ERR_UNSUPPORTED,
+                "iq2_dequantize_to_f16 variant %s is not implemented by the ROCm backend "
+                "(Iq2Xxs only)",
+                variant_name((int)variant));
+  }
+  if (out_dtype != CMK_F32 && out_dtype != CMK_F16 && out_dtype != CMK_BF16)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize unsupported output dtype: %d",
+                (int)out_dtype);
+  const size_t bpr = (in_dim + 255) / 256;
+  size_t blocks, expected_bytes, expected_scales, total;
+  if (!checked_mul(out_dim, bpr, &blocks) || !checked_mul(blocks, 64, &expected_bytes))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 bytes size overflow");
+  if (!checked_mul(blocks, 2, &expected_scales))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 scales size overflow");
+  if (weight_bytes_len < expected_bytes)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "iq2_dequantize_to_f16 weight_bytes too small: got %zu expected at least %zu",
+                weight_bytes_len, expected_bytes);
+  if (weight_scales_len < expected_scales)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "iq2_dequantize_to_f16 weight_scales too small: got %zu expected at least %zu",
+                weight_scales_len, expected_scales);
+  if (!checked_mul(out_dim, in_dim, &total))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 output size overflow");
+  if (out_dim > UINT32_MAX) return fail(CMK_ERR_INVALID_ARGUMENT, "out_dim too large");
+  if (in_dim > UINT32_MAX) return fail(CMK_ERR_INVALID_ARGUMENT, "in_dim too large");
+  if (!weight_bytes || !weight_scales || !out)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 null pointer argument");
+  if (!aligned(weight_bytes, 8) || !aligned(weight_scales, 2))
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "iq2_dequantize_to_f16 needs 8-byte aligned weight_bytes and 2-byte aligned "
+                "weight_scales");
+  if (!aligned(out, out_dtype == CMK_F32 ? 4 : 2))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 out is misaligned");
+  int cus = 0;
+  int rc = current_cu_count(&cus);
+  if (rc != CMK_OK) return rc;
+  hipError_t e = cmk::launch_iq2xxs_dequant(weight_bytes, weight_scales, out, (int)out_dtype,
+                                            (uint32_t)out_dim, (uint32_t)in_dim, cus,
+                                            static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "iq2_dequantize launch");
+  return ok();
+}
+
+// ---- runtime wrappers -----------------------------------------------------
+
+int cmk_device_count(int* count) {
+  if (!count) return fail(CMK_ERR_INVALID_ARGUMENT, "null pointer argument");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) {
+    *count = 0;
+    return fail(CMK_ERR_NO_DEVICE, "hipGetDeviceCount failed: %s", hipGetErrorString(e));
+  }
+  *count = n;
+  return ok();
+}
+
+int cmk_set_device(int ordinal) {
+  hipError_t e = hipSetDevice(ordinal);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipSetDevice");
+}
+
+int cmk_device_props(char* name, size_t name_len, int* cu_count, size_t* lds_bytes,
+                     int* mem_clock_khz, int* mem_bus_bits) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  hipDeviceProp_t p;
+  e = hipGetDeviceProperties(&p, dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  if (name && name_len) snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+  if (cu_count) *cu_count = p.multiProcessorCount;
+  if (lds_bytes) *lds_bytes = p.maxSharedMemoryPerMultiProcessor;
+  if (mem_clock_khz) *mem_clock_khz = p.memoryClockRate;
+  if (mem_bus_bits) *mem_bus_bits = p.memoryBusWidth;
+  return ok();
+}
+
+int cmk_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail(CMK_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipError_t e = hipMalloc(ptr, bytes);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipMalloc");
+}
+
+int cmk_free(void* ptr) {
+  hipError_t e = hipFree(ptr);
+  return e == hipSuccess ? ok() : hip_fail(e, "hipFree");
+}
+
+int cmk_memcpy_htod(void* dst, const void* src, size_t bytes, void* stream) {
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice,
+                                static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipMemcpyAsync(H2D)");
+}
+
+int cmk_memcpy_dtoh(void* dst, const void* src, size_t bytes, void* stream) {
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost,
+                                static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipMemcpyAsync(D2H)");
+}
+
+int cmk_memset(void* dst, int value, size_t bytes, void* stream) {
+  hipError_t e = hipMemsetAsync(dst, value, bytes, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipMemsetAsync");
+}
+
+int cmk_stream_create(void** stream) {
+  if (!stream) return fail(CMK_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipStream_t s = nullptr;
+  hipError_t e = hipStreamCreate(&s);  // default priority
+  if (e != hipSuccess) return hip_fail(e, "hipStreamCreate");
+  *stream = s;
+  return ok();
+}
+
+int cmk_stream_destroy(void* stream) {
+  hipError_t e = hipStreamDestroy(static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamDestroy");
+}
+
+int cmk_stream_synchronize(void* stream) {
+  hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipStreamSynchronize");
+}
+
+int cmk_device_synchronize(void) {
+  hipError_t e = hipDeviceSynchronize();
+  return e == hipSuccess ? ok() : hip_fail(e, "hipDeviceSynchronize");
+}
+
+int cmk_event_create(void** event) {
+  if (!event) return fail(CMK_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreate(&ev);
+  if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+  *event = ev;
+  return ok();
+}
+
+int cmk_event_destroy(void* event) {
+  hipError_t e = hipEventDestroy(static_cast<hipEvent_t>(event));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipEventDestroy");
+}
+
+int cmk_event_record(void* event, void* stream) {
+  hipError_t e = hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipEventRecord");
+}
+
+int cmk_event_elapsed_ms(void* start, void* stop, float* ms) {
+  if (!ms) return fail(CMK_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipError_t e = hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                                     static_cast<hipEvent_t>(stop));
+  return e == hipSuccess ? ok() : hip_fail(e, "hipEventElapsedTime");
+}
+
+}  // extern "C"

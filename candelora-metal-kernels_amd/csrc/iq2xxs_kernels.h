@@ -1,0 +1,43 @@
+// iq2xxs_kernels.h — internal launcher interface between the C ABI (cmk_iq2.cpp)
+// and the HIP kernels.  Not part of the public ABI (include/cmk_iq2.h).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cmk {
+
+// dtype / output kind codes shared with the ABI: 0 = f32, 1 = f16, 2 = bf16.
+
+// Dense dequantisation, out[out_dim, in_dim].  Needs 8-byte aligned
+// weight_bytes and 2-byte aligned weight_scales.
+hipError_t launch_iq2xxs_dequant(const uint8_t* wb, const uint8_t* ws, void* out, int out_kind,
+                                 uint32_t out_dim, uint32_t in_dim, int num_cus,
+                                 hipStream_t stream);
+
+// Decode-shaped matmul (int8-MFMA GEMV), any m, in_dim <= 32768 (gemv_supported).
+// Needs 16-byte aligned weight_bytes and 2-byte aligned weight_scales.
+bool gemv_supported(uint32_t in_dim);
+size_t gemv_lds_bytes(uint32_t in_dim, uint32_t rg_per_wg, uint32_t slices);
+hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                              const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
+                              bool w8a8, int num_cus, hipStream_t stream);
+
+// W8A8 per-row inverse scale: inv[r] = 127 / max|x_r| (1 when max < 1e-8).
+hipError_t launch_iq2xxs_row_inv_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
+                                       float* inv_out, hipStream_t stream);
+
+// Portable matmul for any alignment / shape (one wave per output row).
+// row_inv: W8A8 per-row scales (from launch_iq2xxs_row_inv_scale) or null.
+hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                                       const uint8_t* ws, float* out, uint32_t out_dim,
+                                       uint32_t in_dim, const float* row_inv, int num_cus,
+                                       hipStream_t stream);
+
+// Prefill matmul (MFMA GEMM, weights dequantised into LDS as f16/bf16);
+// x_dtype must be 1 (f16) or 2 (bf16).  Needs 8-byte aligned weight_bytes.
+hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                              const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
+                              const float* row_inv, hipStream_t stream);
+
+}  // namespace cmk

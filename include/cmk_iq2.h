@@ -1,0 +1,164 @@
+/*
+ * cmk_iq2.h — C ABI of the MI355X (gfx950) IQ2_XXS matmul library, libcmk_iq2.so.
+ *
+ * This is the drop-in boundary for the crate candelora-metal-kernels: the
+ * crate keeps its public Rust API (module candelora_metal_kernels::iq2_matmul,
+ * src/iq2_matmul.rs:31-37,535-670; candelora_metal_kernels::activation_quant,
+ * src/activation_quant.rs:7-44) and, under a `rocm` cargo feature, its bodies
+ * call the entry points below instead of the Metal dispatch helpers
+ * iq2_matmul_metal (src/iq2_matmul.rs:197-365) and
+ * iq2_dequantize_to_f16_metal (src/iq2_matmul.rs:367-505).
+ *
+ * Conventions
+ *  - Plain pointers and sizes only.  Device pointers are HIP device memory
+ *    (from cmk_device_malloc or any hipMalloc'd buffer); `stream` is a
+ *    hipStream_t passed as void* (NULL = the default stream).
+ *  - Launch entry points are asynchronous on `stream` and never allocate
+ *    device memory.  Callers synchronise (cmk_stream_synchronize), the same
+ *    contract as the reference's encoder-based dispatch, whose callers call
+ *    device.synchronize() (src/iq2_matmul.rs:1101).
+ *  - Return value: CMK_OK (0) or a negative cmk_status.  On error the
+ *    message is available from cmk_last_error() (thread-local, valid until the
+ *    next call on the same thread).  Message texts follow the reference's
+ *    bail! texts (src/iq2_matmul.rs:210-311,367-433).
+ *  - Thread safety: entry points may be called concurrently from several
+ *    host threads; launches on the same stream are ordered by that stream.
+ */
+#ifndef CMK_IQ2_H
+#define CMK_IQ2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CMK_IQ2_ABI_VERSION 1
+
+/* Status codes. */
+typedef enum cmk_status {
+    CMK_OK = 0,
+    CMK_ERR_INVALID_ARGUMENT = -1, /* shape/size/dtype contract violated */
+    CMK_ERR_UNSUPPORTED = -2,      /* a variant or mode this build does not implement */
+    CMK_ERR_HIP = -3,              /* a HIP runtime call failed */
+    CMK_ERR_NO_DEVICE = -4         /* no usable gfx950 device */
+} cmk_status;
+
+/* Element types of x / the dequantized output.  Mirrors the candle DTypes the
+ * reference accepts for x: F32, F16, BF16 (src/iq2_matmul.rs:59-75). */
+typedef enum cmk_dtype { CMK_F32 = 0, CMK_F16 = 1, CMK_BF16 = 2 } cmk_dtype;
+
+/* Iq2MatmulVariant (src/iq2_matmul.rs:31-37).  Only IQ2_XXS is implemented;
+ * the others return CMK_ERR_UNSUPPORTED. */
+typedef enum cmk_iq2_variant {
+    CMK_IQ2_XXS = 0,
+    CMK_IQ2_XS = 1,
+    CMK_IQ2_S = 2,
+    CMK_IQ3_S = 3
+} cmk_iq2_variant;
+
+/* ActivationQuantMode (src/activation_quant.rs:7-15). */
+typedef enum cmk_act_quant_mode {
+    CMK_ACT_QUANT_OFF = 0,
+    CMK_ACT_QUANT_W8A8 = 1,
+    CMK_ACT_QUANT_W4A8 = 2
+} cmk_act_quant_mode;
+
+/* ------------------------------------------------------------------------ */
+/* Launch entry points                                                       */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * out[m, out_dim] (fp32) = x[m, in_dim] . W^T, W the IQ2_XXS matrix
+ * [out_dim, in_dim] held as the reference's split super-blocks:
+ *   weight_bytes : out_dim * ceil(in_dim/256) blocks x 64 B (32 x u16 qs)
+ *   weight_scales: out_dim * ceil(in_dim/256) blocks x 2 B (fp16 d, LE)
+ * (src/iq2_matmul.rs:13-17; block index = row * blocks_per_row + blk).
+ *
+ * Replaces iq2_matmul_metal (src/iq2_matmul.rs:197-365) as reached from
+ * iq2_matmul / iq2_xxs_matmul (:535-553, :604-619) with mode OFF, and from
+ * iq2_matmul_with_activation_quant (:559-591) for every mode:
+ *   OFF  -> plain matmul;
+ *   W8A8 -> x is first fake-quantised per row (inv = 127/max|x_row|, or 1 when
+ *           max < 1e-8; q = clamp(round_half_away(x*inv), +-127); x' = q/inv),
+ *           iq2_matmul.metal:85-126;
+ *   W4A8 -> error when `strict` != 0, else runs as OFF (:581-589).
+ * x_len / weight_bytes_len / weight_scales_len are the element counts the
+ * caller's buffers hold; like the reference, larger weight buffers are fine
+ * (:237-259) and x must hold at least m*in_dim elements.
+ * Dimensions must be non-zero and fit in u32 (:210-212, :305-311).
+ * `workspace` may be NULL when cmk_iq2_matmul_workspace_size reports 0.
+ */
+int cmk_iq2_matmul(const void *x, cmk_dtype x_dtype, size_t x_len, size_t m,
+                   const uint8_t *weight_bytes, size_t weight_bytes_len,
+                   const uint8_t *weight_scales, size_t weight_scales_len,
+                   size_t out_dim, size_t in_dim, cmk_iq2_variant variant,
+                   cmk_act_quant_mode mode, int strict,
+                   float *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Device scratch (bytes) that cmk_iq2_matmul needs for these arguments.  The
+ * launch never allocates; callers that get a non-zero size pass a buffer of at
+ * least that many bytes.  Same argument validation as cmk_iq2_matmul. */
+int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, size_t in_dim,
+                                  cmk_iq2_variant variant, cmk_act_quant_mode mode,
+                                  size_t *bytes);
+
+/*
+ * out[out_dim, in_dim] = dequantised W in out_dtype (F16, BF16 or F32).
+ * Replaces iq2_dequantize_to_f16_metal (src/iq2_matmul.rs:367-505) reached
+ * from iq2_dequantize_to_f16 (:594-602), whose kernel is
+ * iq2_xxs_dequantize_f16 (iq2_matmul.metal:868-887).  Every value is the
+ * single round-to-nearest-even of the exact product d*(0.5+s)*0.25*g*sign;
+ * F32 output is that exact product.  F16 is the reference's output type;
+ * BF16/F32 are this build's extensions on the same boundary.
+ */
+int cmk_iq2_dequantize(const uint8_t *weight_bytes, size_t weight_bytes_len,
+                       const uint8_t *weight_scales, size_t weight_scales_len,
+                       size_t out_dim, size_t in_dim, cmk_iq2_variant variant,
+                       cmk_dtype out_dtype, void *out, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Errors and introspection                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *cmk_last_error(void);
+/* CMK_IQ2_ABI_VERSION of the loaded library. */
+int cmk_abi_version(void);
+/* Which kernel family cmk_iq2_matmul picks for these arguments:
+ * 0 = GEMV (small m), 1 = MFMA GEMM.  Host-only, no device needed. */
+int cmk_iq2_matmul_path(cmk_dtype x_dtype, size_t m, size_t out_dim, size_t in_dim,
+                        cmk_act_quant_mode mode);
+
+/* ------------------------------------------------------------------------ */
+/* Thin HIP runtime wrappers for hosts that do not link HIP themselves (the   */
+/* Rust crate's src/hip/ffi.rs).  All return cmk_status.                      */
+/* ------------------------------------------------------------------------ */
+
+int cmk_device_count(int *count);
+int cmk_set_device(int ordinal);
+/* Name, CU count, LDS bytes per workgroup, peak memory clock (kHz) and bus
+ * width (bits) of the current device; name_len includes the terminator. */
+int cmk_device_props(char *name, size_t name_len, int *cu_count, size_t *lds_bytes,
+                     int *mem_clock_khz, int *mem_bus_bits);
+int cmk_malloc(void **ptr, size_t bytes);
+int cmk_free(void *ptr);
+int cmk_memcpy_htod(void *dst, const void *src, size_t bytes, void *stream);
+int cmk_memcpy_dtoh(void *dst, const void *src, size_t bytes, void *stream);
+int cmk_memset(void *dst, int value, size_t bytes, void *stream);
+int cmk_stream_create(void **stream);
+int cmk_stream_destroy(void *stream);
+int cmk_stream_synchronize(void *stream);
+int cmk_device_synchronize(void);
+int cmk_event_create(void **event);
+int cmk_event_destroy(void *event);
+int cmk_event_record(void *event, void *stream);
+/* Milliseconds between two recorded, completed events. */
+int cmk_event_elapsed_ms(void *start, void *stop, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CMK_IQ2_H */

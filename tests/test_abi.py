@@ -1,0 +1,136 @@
+"""The C ABI on the host: the library loads, exports every symbol that
+include/cmk_iq2.h declares, and rejects invalid arguments with the reference's
+error texts before touching any device (so these run without a GPU)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "cmk_iq2.h")
+
+
+def declared_symbols():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(cmk_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol(cabi):
+    L = cabi.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    for s in syms:
+        assert hasattr(L, s), s
+    assert sorted(cabi.EXPORTED) == syms
+    assert L.cmk_abi_version() == 1
+
+
+NULL = None
+
+
+def call(cabi, **kw):
+    args = dict(x=NULL, x_dtype=0, x_len=0, m=1, wb=NULL, wb_len=1 << 20, ws=NULL, ws_len=1 << 20,
+                out_dim=7, in_dim=320, variant=0, mode=0, strict=0, out=NULL, work=NULL,
+                work_bytes=0, stream=NULL)
+    args.update(kw)
+    rc = cabi.lib().cmk_iq2_matmul(args["x"], args["x_dtype"], args["x_len"], args["m"],
+                                   args["wb"], args["wb_len"], args["ws"], args["ws_len"],
+                                   args["out_dim"], args["in_dim"], args["variant"], args["mode"],
+                                   args["strict"], args["out"], args["work"], args["work_bytes"],
+                                   args["stream"])
+    return rc, cabi.last_error()
+
+
+def test_zero_dims(cabi):
+    for od, idim in ((0, 320), (7, 0)):
+        rc, msg = call(cabi, out_dim=od, in_dim=idim)
+        assert rc == cabi.CMK_ERR_INVALID_ARGUMENT
+        assert msg == "iq2_matmul expects non-zero dimensions"
+
+
+def test_w4a8_strict_and_fallback(cabi):
+    rc, msg = call(cabi, mode=cabi.CMK_ACT_QUANT_W4A8, strict=1)
+    assert rc == cabi.CMK_ERR_UNSUPPORTED
+    assert msg == ("activation quant mode W4A8 requested in strict mode, but W4A8 kernel path is "
+                   "not implemented yet")
+    # non-strict W4A8 runs as Off: it reaches the Off path's own checks
+    rc, msg = call(cabi, mode=cabi.CMK_ACT_QUANT_W4A8, strict=0, out_dim=0)
+    assert msg == "iq2_matmul expects non-zero dimensions"
+
+
+def test_other_variants_unsupported(cabi):
+    for v, name in ((1, "Iq2Xs"), (2, "Iq2S"), (3, "Iq3S")):
+        rc, msg = call(cabi, variant=v)
+        assert rc == cabi.CMK_ERR_UNSUPPORTED and name in msg
+    rc, msg = call(cabi, variant=9)
+    assert rc == cabi.CMK_ERR_INVALID_ARGUMENT
+
+
+def test_bad_dtype(cabi):
+    rc, msg = call(cabi, x_dtype=7)
+    assert rc == cabi.CMK_ERR_INVALID_ARGUMENT and msg == "iq2_matmul unsupported x dtype: 7"
+    rc, msg = call(cabi, x_dtype=7, mode=cabi.CMK_ACT_QUANT_W8A8)
+    assert msg == "iq2_matmul_w8a8 unsupported x dtype: 7"
+
+
+def test_buffer_sizes(cabi):
+    # N=7, K=320 -> 7 rows x 2 blocks: 896 bytes, 28 scale bytes (src/iq2_matmul.rs:237-259)
+    rc, msg = call(cabi, wb_len=895, ws_len=28)
+    assert rc == cabi.CMK_ERR_INVALID_ARGUMENT
+    assert msg == "iq2_matmul weight_bytes too small: got 895 expected at least 896"
+    rc, msg = call(cabi, wb_len=896, ws_len=27)
+    assert msg == "iq2_matmul weight_scales too small: got 27 expected at least 28"
+    rc, msg = call(cabi, wb_len=896, ws_len=28, x_len=639, m=2)
+    assert msg == "iq2_matmul x too small: got 639 expected at least 640"
+    rc, msg = call(cabi, wb_len=896, ws_len=28, x_len=640, m=2)
+    assert msg == "iq2_matmul null pointer argument"
+
+
+def test_overflow_and_u32_limits(cabi):
+    rc, msg = call(cabi, out_dim=1 << 62, in_dim=1 << 40)
+    assert msg == "iq2_matmul bytes size overflow"
+    rc, msg = call(cabi, m=1 << 32, out_dim=1, in_dim=256, wb_len=64, ws_len=2)
+    assert msg == "m too large"
+    rc, msg = call(cabi, m=1, out_dim=1 << 32, in_dim=256, wb_len=1 << 40, ws_len=1 << 40)
+    assert msg == "out_dim too large"
+
+
+def test_empty_activation_is_a_noop(cabi):
+    rc, msg = call(cabi, m=0, wb_len=896, ws_len=28)
+    assert rc == cabi.CMK_OK and msg == ""
+
+
+def test_dequantize_validation(cabi):
+    L = cabi.lib()
+
+    def dq(**kw):
+        a = dict(wb=NULL, wbl=896, ws=NULL, wsl=28, od=7, idim=320, v=0, dt=1, out=NULL)
+        a.update(kw)
+        rc = L.cmk_iq2_dequantize(a["wb"], a["wbl"], a["ws"], a["wsl"], a["od"], a["idim"], a["v"],
+                                  a["dt"], a["out"], NULL)
+        return rc, cabi.last_error()
+
+    assert dq(od=0)[1] == "iq2_dequantize_to_f16 expects non-zero dimensions"
+    assert dq(wbl=10)[1] == ("iq2_dequantize_to_f16 weight_bytes too small: got 10 expected at "
+                             "least 896")
+    assert dq(wsl=1)[1] == ("iq2_dequantize_to_f16 weight_scales too small: got 1 expected at "
+                            "least 28")
+    assert dq(v=2)[0] == cabi.CMK_ERR_UNSUPPORTED
+    assert "unsupported output dtype" in dq(dt=5)[1]
+    assert dq()[1] == "iq2_dequantize_to_f16 null pointer argument"
+
+
+def test_workspace_and_path_queries(cabi):
+    assert cabi.workspace_size(cabi.CMK_F16, 512, 14336, 4096) == 0
+    assert cabi.workspace_size(cabi.CMK_F16, 512, 14336, 4096, mode=cabi.CMK_ACT_QUANT_W8A8) == 2048
+    assert cabi.workspace_size(cabi.CMK_F32, 1, 4096, 4096, mode=cabi.CMK_ACT_QUANT_OFF) == 0
+    assert cabi.matmul_path(cabi.CMK_F16, 512, 14336, 4096) == "gemm"
+    assert cabi.matmul_path(cabi.CMK_BF16, 17, 14336, 4096) == "gemm"
+    assert cabi.matmul_path(cabi.CMK_F16, 16, 14336, 4096) == "gemv"
+    assert cabi.matmul_path(cabi.CMK_F32, 1, 14336, 4096) == "gemv"
+    with pytest.raises(cabi.CmkError):
+        cabi.workspace_size(cabi.CMK_F16, 1, 0, 4096)

@@ -1,0 +1,257 @@
+"""GPU parity of the HIP path against the CPU oracle (gfx950 only).
+
+Bars:
+  * dequantisation: bit-exact (f16, bf16, f32) against the oracle;
+  * reference in-test cases (src/iq2_matmul.rs:1065-1253): |gpu - oracle| <= 2e-3
+    (mode Off) and <= 3e-3 (W8A8), the reference's own tolerances;
+  * GEMV (x f32 or any x at small m): error measured against the fp64-accumulated
+    oracle with two metrics, both written in the asserts:
+      cond  = max_i |y_i - y64_i| / sum_k |x_k w_ik|   (<= 1e-5, fp32 class)
+      rel   = max over outputs with |y64_i| >= 1e-2 max|y64| of |y_i - y64_i|/|y64_i|
+              (<= 1e-3, the GEMV bar)
+  * MFMA GEMM (x f16/bf16, large m): against x @ dequant_{f16,bf16}(W)^T in fp64
+    with cond <= 1e-4 and rel <= 1e-2 (the GEMM bar).
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def dev(pkg):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    pkg.cabi.lib()  # fail loudly when the HIP library is missing
+    return torch.device("cuda:0")
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def x_tensor(x_f32, dtype, dev):
+    t = torch.from_numpy(np.ascontiguousarray(x_f32)).to(dev)
+    return t.to(dtype)
+
+
+def x_as_f32(xt):
+    return xt.float().cpu().numpy()
+
+
+def errors(y, y64, scale):
+    y = np.asarray(y, np.float64)
+    cond = float(np.max(np.abs(y - y64) / np.maximum(scale, 1e-300)))
+    big = np.abs(y64) >= 1e-2 * np.max(np.abs(y64))
+    rel = float(np.max(np.abs(y - y64)[big] / np.abs(y64[big]))) if big.any() else 0.0
+    return cond, rel
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("out_dim,in_dim", [(7, 320), (64, 4096), (5, 41), (3, 300), (33, 8192)])
+def test_dequant_bit_exact(pkg, oracle, inputs, dev, out_dim, in_dim):
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim, seed=out_dim * 31 + in_dim)
+    wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
+    f16 = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs)
+    assert f16.dtype == torch.float16 and tuple(f16.shape) == (out_dim, in_dim)
+    got = f16.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, oracle.dequantize_f16_bits(wb, ws, out_dim, in_dim))
+    bf = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                   out_dtype=torch.bfloat16)
+    got = bf.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, oracle.dequantize_bf16_bits(wb, ws, out_dim, in_dim))
+    f32 = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                    out_dtype=torch.float32)
+    assert np.array_equal(f32.cpu().numpy().view(np.uint32),
+                          oracle.dequantize_f32(wb, ws, out_dim, in_dim).view(np.uint32))
+
+
+def test_dequant_reference_case_matches_golden(pkg, oracle, dev):
+    import hashlib
+    import json
+    import os
+    from conftest import REPO
+    pc = json.load(open(os.path.join(REPO, "tests", "golden", "reference_cases.json")))["parity_case"]
+    _, wb, ws = oracle.reference_case_inputs()
+    f16 = pkg.iq2_dequantize_to_f16(to_dev(wb, dev), to_dev(ws, dev), 7, 320,
+                                    pkg.Iq2MatmulVariant.Iq2Xxs)
+    bits = f16.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert hashlib.sha256(bits.tobytes()).hexdigest() == pc["dequant_f16_sha256"]
+
+
+# ------------------------------------------------------------------ reference cases
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_cpu_vs_hip_parity_iq2_xxs(pkg, oracle, dev, dtype):
+    x, wb, ws = oracle.reference_case_inputs()
+    xt = x_tensor(x, dtype, dev)
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), 7, 320, pkg.Iq2MatmulVariant.Iq2Xxs)
+    torch.cuda.synchronize()
+    ref = oracle.matmul_reference(x_as_f32(xt), 2, 7, 320, wb, ws)
+    diff = np.abs(y.cpu().numpy() - ref)
+    assert diff.max() <= 2e-3, diff.max()  # src/iq2_matmul.rs:1113,1121
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_cpu_vs_hip_parity_w8a8_iq2_xxs(pkg, oracle, dev, dtype):
+    x, wb, ws = oracle.reference_case_inputs()
+    xt = x_tensor(x, dtype, dev)
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(xt, to_dev(wb, dev), to_dev(ws, dev), 7, 320,
+                                             pkg.Iq2MatmulVariant.Iq2Xxs, cfg)
+    ref = oracle.matmul_reference_w8a8(x_as_f32(xt), 2, 7, 320, wb, ws)
+    diff = np.abs(y.cpu().numpy() - ref)
+    assert diff.max() <= 3e-3, diff.max()  # src/iq2_matmul.rs:1239,1247
+
+
+def test_w8a8_kernel_smoke_iq2_xxs(pkg, oracle, dev):
+    x, wb, ws = oracle.reference_case_inputs(2, 6, 320, 0x0BADC0DE, 0xD15EA5ED, 0xC3)
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), 6,
+                                             320, pkg.Iq2MatmulVariant.Iq2Xxs, cfg)
+    yh = y.cpu().numpy()
+    assert yh.shape == (2, 6) and np.all(np.isfinite(yh))
+
+
+def test_w4a8_non_strict_runs_as_off_and_strict_errors(pkg, oracle, dev):
+    x, wb, ws = oracle.reference_case_inputs()
+    args = (to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), 7, 320, pkg.Iq2MatmulVariant.Iq2Xxs)
+    off = pkg.iq2_matmul(*args)
+    w4 = pkg.iq2_matmul_with_activation_quant(
+        *args, pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W4A8, False))
+    assert torch.equal(off, w4)
+    with pytest.raises(pkg.Iq2MatmulError, match="strict mode"):
+        pkg.iq2_matmul_with_activation_quant(
+            *args, pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W4A8, True))
+
+
+# ------------------------------------------------------------------ GEMV (small m)
+
+GEMV_CASES = [
+    (1, 4096, 4096),     # config 0
+    (1, 14336, 4096),    # config 1 gate/up
+    (1, 4096, 14336),    # config 1 down
+    (4, 4096, 4096),     # config 2
+    (8, 1024, 4096),
+    (16, 512, 4096),
+    (3, 13, 300),        # ragged N, partial block
+    (1, 6, 41),          # K < one sub-block
+    (2, 1028, 28672),    # config 4 down-proj K
+]
+
+
+@pytest.mark.parametrize("m,out_dim,in_dim", GEMV_CASES)
+def test_gemv_f32_vs_fp64_oracle(pkg, oracle, inputs, dev, m, out_dim, in_dim):
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    x = inputs.synthetic_x(m, in_dim)
+    y = pkg.iq2_matmul(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    y64, sc = oracle.matmul_f64(x, m, out_dim, in_dim, wb, ws)
+    cond, rel = errors(y, y64, sc)
+    assert cond <= 1e-5, cond
+    assert rel <= 1e-3, rel
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gemv_half_x(pkg, oracle, inputs, dev, dtype):
+    m, out_dim, in_dim = 1, 2048, 4096
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim), dtype, dev)
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    y64, sc = oracle.matmul_f64(x_as_f32(xt), m, out_dim, in_dim, wb, ws)
+    cond, rel = errors(y, y64, sc)
+    assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+
+
+def test_gemv_w8a8_vs_oracle(pkg, oracle, inputs, dev):
+    m, out_dim, in_dim = 2, 4096, 4096
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    x = inputs.synthetic_x(m, in_dim)
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev),
+                                             out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                             cfg).cpu().numpy()
+    xq = oracle.rowwise_qdq_w8a8(x, m, in_dim)
+    y64, sc = oracle.matmul_f64(xq, m, out_dim, in_dim, wb, ws)
+    cond, rel = errors(y, y64, sc)
+    assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+
+
+def test_rank1_x_and_empty_m(pkg, oracle, inputs, dev):
+    wb, ws = inputs.synthetic_weights(64, 512)
+    x = inputs.synthetic_x(1, 512)
+    y1 = pkg.iq2_matmul(to_dev(x[0], dev), to_dev(wb, dev), to_dev(ws, dev), 64, 512,
+                        pkg.Iq2MatmulVariant.Iq2Xxs)
+    assert tuple(y1.shape) == (64,)
+    y2 = pkg.iq2_matmul(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), 64, 512,
+                        pkg.Iq2MatmulVariant.Iq2Xxs)
+    assert torch.equal(y1, y2[0])
+    y0 = pkg.iq2_matmul(torch.zeros((0, 512), device=dev), to_dev(wb, dev), to_dev(ws, dev), 64,
+                        512, pkg.Iq2MatmulVariant.Iq2Xxs)
+    assert tuple(y0.shape) == (0, 64)
+    with pytest.raises(pkg.Iq2MatmulError, match="rank 1 or 2"):
+        pkg.iq2_matmul(torch.zeros((1, 1, 512), device=dev), to_dev(wb, dev), to_dev(ws, dev),
+                       64, 512, pkg.Iq2MatmulVariant.Iq2Xxs)
+
+
+def test_unaligned_weights_take_portable_path(pkg, oracle, inputs, dev):
+    m, out_dim, in_dim = 2, 37, 512
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    big_b = torch.zeros(wb.size + 1, dtype=torch.uint8, device=dev)
+    big_b[1:] = to_dev(wb, dev)
+    x = inputs.synthetic_x(m, in_dim)
+    y = pkg.iq2_matmul(to_dev(x, dev), big_b[1:], to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    y64, sc = oracle.matmul_f64(x, m, out_dim, in_dim, wb, ws)
+    cond, rel = errors(y, y64, sc)
+    assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+
+
+def test_deterministic(pkg, inputs, dev):
+    wb, ws = inputs.synthetic_weights(4096, 4096)
+    x = to_dev(inputs.synthetic_x(1, 4096), dev)
+    a = pkg.iq2_xxs_matmul(x, to_dev(wb, dev), to_dev(ws, dev), 4096, 4096)
+    b = pkg.iq2_xxs_matmul(x, to_dev(wb, dev), to_dev(ws, dev), 4096, 4096)
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ MFMA GEMM (large m)
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,out_dim,in_dim", [(512, 1024, 4096), (100, 300, 1000), (17, 64, 320)])
+def test_gemm_vs_dequant_matmul(pkg, oracle, inputs, dev, dtype, m, out_dim, in_dim):
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim), dtype, dev)
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F16, m, out_dim, in_dim) == "gemm"
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    if dtype == torch.float16:
+        w = oracle.dequantize_f16_bits(wb, ws, out_dim, in_dim).view(np.float16).astype(np.float64)
+    else:
+        wbits = oracle.dequantize_bf16_bits(wb, ws, out_dim, in_dim).astype(np.uint32) << 16
+        w = wbits.view(np.float32).astype(np.float64)
+    x64 = x_as_f32(xt).astype(np.float64)
+    y64 = x64 @ w.T
+    sc = np.abs(x64) @ np.abs(w).T
+    cond, rel = errors(y, y64, sc)
+    assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+
+
+def test_gemm_w8a8(pkg, oracle, inputs, dev):
+    m, out_dim, in_dim = 64, 256, 1024
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim) * 3, torch.float16, dev)
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim,
+                                             in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                             cfg).cpu().numpy()
+    xq = oracle.rowwise_qdq_w8a8(x_as_f32(xt), m, in_dim).astype(np.float64)
+    w = oracle.dequantize_f16_bits(wb, ws, out_dim, in_dim).view(np.float16).astype(np.float64)
+    y64 = xq @ w.T
+    cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
+    assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
