@@ -5,8 +5,7 @@ Every HIP source is compiled with hipcc for gfx950 only; objects go to
 candelora-metal-kernels_amd/_build/, the shared libraries next to this file.
 
   libcmk_iq2.so        C ABI (include/cmk_iq2.h): kernels + dispatch + runtime wrappers
-  libcandelora_iq2.so  C++ mirror of the reference's Rust API (host/), linked to libcmk_iq2
-  iq2_matmul_tests     C++ test driver for the host layer (tests/cpp/)
+  libcandelora_iq2.so  C++ host layer with the reference's API (host/), linked to libcmk_iq2
 """
 
 from __future__ import annotations
@@ -26,7 +25,6 @@ INCLUDE = os.path.join(REPO, "include")
 
 LIB = os.path.join(PKG, "libcmk_iq2.so")
 HOST_LIB = os.path.join(PKG, "libcandelora_iq2.so")
-TEST_BIN = os.path.join(PKG, "iq2_matmul_tests")
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -81,24 +79,18 @@ def build_lib() -> str:
     return LIB
 
 
-def build_host() -> tuple[str, str]:
-    """C++ mirror of the reference API + its test driver (host code only)."""
+def build_host() -> str:
+    """C++ host layer with the reference API (host code only, over the C ABI)."""
     host_src = os.path.join(HOST, "iq2_matmul.cpp")
     if not os.path.exists(host_src):
-        return "", ""
+        return ""
     rocm_inc = "/opt/rocm/include"
     cxx = ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", f"-I{INCLUDE}", f"-I{HOST}",
            f"-I{rocm_inc}"]
     tmp = HOST_LIB + ".tmp"
     _run([*cxx, "-shared", "-o", tmp, host_src, f"-L{PKG}", "-lcmk_iq2", "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, HOST_LIB)
-    test_src = os.path.join(REPO, "tests", "cpp", "iq2_matmul_tests.cpp")
-    if os.path.exists(test_src):
-        tmpb = TEST_BIN + ".tmp"
-        _run([*cxx, "-o", tmpb, test_src, f"-L{PKG}", "-lcandelora_iq2", "-lcmk_iq2",
-              "-Wl,-rpath,$ORIGIN"])
-        os.replace(tmpb, TEST_BIN)
-    return HOST_LIB, TEST_BIN
+    return HOST_LIB
 
 
 def build() -> str:
@@ -111,7 +103,7 @@ def build() -> str:
 
 def clean() -> None:
     shutil.rmtree(OBJ, ignore_errors=True)
-    for p in (LIB, HOST_LIB, TEST_BIN):
+    for p in (LIB, HOST_LIB):
         if os.path.exists(p):
             os.remove(p)
 

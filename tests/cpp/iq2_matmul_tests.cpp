@@ -1,0 +1,295 @@
+// iq2_matmul_tests.cpp — tests of the C++ host layer, named after the reference's
+// own tests (src/iq2_matmul.rs:1255-1313, src/lib.rs:7-13).
+//
+// Usage: iq2_matmul_tests [--host | --gpu | --all | NAME...]
+//   --host  tests that never touch a device (argument errors, API contracts)
+//   --gpu   tests that run kernels (need an MI355X)
+// The CPU oracle (oracle/, test infrastructure) is the reference side of every
+// parity test, with the reference's tolerances.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "candelora/iq2_matmul.hpp"
+#include "iq2xxs_oracle.h"
+
+using namespace candelora;
+
+namespace {
+
+struct Failure {
+  std::string what;
+};
+
+#define CHECK(cond, msg)                                                                     \
+  do {                                                                                       \
+    if (!(cond)) throw Failure{std::string(__FILE__) + ":" + std::to_string(__LINE__) + ": " + \
+                               (msg)};                                                       \
+  } while (0)
+
+template <class F>
+std::string expect_error(F&& f) {
+  try {
+    f();
+  } catch (const Error& e) {
+    return e.what();
+  }
+  throw Failure{"expected candelora::Error, got success"};
+}
+
+struct Case {
+  std::vector<float> x;
+  std::vector<uint8_t> wb, ws;
+  size_t m, out_dim, in_dim;
+};
+
+// Inputs of parity_case / w8a8_smoke_case (src/iq2_matmul.rs:1071-1086, 1136-1146).
+Case reference_case(size_t m, size_t out_dim, size_t in_dim, uint32_t bseed, uint32_t sseed,
+                    uint8_t tail) {
+  Case c{{}, {}, {}, m, out_dim, in_dim};
+  const size_t bpr = (in_dim + 255) / 256, nb = out_dim * bpr;
+  c.wb.resize(nb * 64);
+  c.ws.resize(nb * 2);
+  oracle_lcg_fill(c.wb.data(), c.wb.size(), bseed);
+  oracle_lcg_fill(c.ws.data(), c.ws.size(), sseed);
+  oracle_force_f16_one_per_block(c.ws.data(), c.ws.size(), 2);
+  if (!c.wb.empty()) c.wb.back() = tail;
+  c.x.resize(m * in_dim);
+  oracle_deterministic_x(c.x.data(), c.x.size());
+  return c;
+}
+
+Case parity_inputs() { return reference_case(2, 7, 320, 0xA11CE5ED, 0xC0FFEE12, 0x5A); }
+
+struct DevCase {
+  Tensor x, wb, ws;
+};
+
+DevCase upload(const Case& c, const Device& dev) {
+  return {Tensor::from_vec(c.x, {c.m, c.in_dim}, DType::F32, dev),
+          Tensor::from_vec(c.wb, {c.wb.size()}, DType::U8, dev),
+          Tensor::from_vec(c.ws, {c.ws.size()}, DType::U8, dev)};
+}
+
+double max_abs_diff(const std::vector<float>& a, const std::vector<float>& b) {
+  CHECK(a.size() == b.size(), "size mismatch");
+  double m = 0;
+  for (size_t i = 0; i < a.size(); ++i) m = std::fmax(m, std::fabs((double)a[i] - b[i]));
+  return m;
+}
+
+// ------------------------------------------------------------------ host tests
+
+void crate_loads() { CHECK(true, "crate loads"); }
+
+void activation_quant_config_contract() {
+  ActivationQuantConfig d;
+  CHECK(d.mode == ActivationQuantMode::Off && !d.strict && !d.is_enabled(), "default is Off");
+  CHECK((ActivationQuantConfig{ActivationQuantMode::W8A8, false}).is_enabled(), "W8A8 enabled");
+  CHECK((ActivationQuantConfig{ActivationQuantMode::W4A8, true}).is_enabled(), "W4A8 enabled");
+}
+
+void errors_before_any_device_access() {
+  Case c = parity_inputs();
+  DevCase h = upload(c, Device::cpu());
+  std::string e = expect_error(
+      [&] { iq2_matmul(h.x, h.wb, h.ws, 0, 320, Iq2MatmulVariant::Iq2Xxs); });
+  CHECK(e == "iq2_matmul expects non-zero dimensions", e);
+  e = expect_error([&] { iq2_matmul(h.x, h.wb, h.ws, 7, 320, Iq2MatmulVariant::Iq2Xxs); });
+  CHECK(e == "iq2_matmul requires a HIP device", e);
+  e = expect_error([&] {
+    iq2_matmul_with_activation_quant(h.x, h.wb, h.ws, 7, 320, Iq2MatmulVariant::Iq2Xxs,
+                                     {ActivationQuantMode::W4A8, true});
+  });
+  CHECK(e == "activation quant mode W4A8 requested in strict mode, but W4A8 kernel path is not "
+             "implemented yet",
+        e);
+  e = expect_error([&] { iq2_dequantize_to_f16(h.wb, h.ws, 7, 0, Iq2MatmulVariant::Iq2Xxs); });
+  CHECK(e == "iq2_dequantize_to_f16 expects non-zero dimensions", e);
+  e = expect_error([&] { iq2_dequantize_to_f16(h.wb, h.ws, 7, 320, Iq2MatmulVariant::Iq2Xxs); });
+  CHECK(e == "iq2_dequantize_to_f16 requires a HIP device", e);
+}
+
+// ------------------------------------------------------------------ GPU tests
+
+void parity_case(Iq2MatmulVariant variant) {
+  Case c = parity_inputs();
+  DevCase d = upload(c, Device::hip(0));
+  Tensor y = iq2_matmul(d.x, d.wb, d.ws, 7, 320, variant);
+  synchronize();
+  std::vector<float> ref(c.m * c.out_dim);
+  oracle_iq2xxs_matmul_reference(c.x.data(), c.m, c.out_dim, c.in_dim, c.wb.data(), c.ws.data(),
+                                 ref.data());
+  CHECK(y.dims() == (std::vector<size_t>{2, 7}), "output shape");
+  CHECK(y.dtype() == DType::F32, "output dtype");
+  const double md = max_abs_diff(y.to_vec<float>(), ref);
+  CHECK(md <= 2e-3, "IQ2 parity max_abs too high: " + std::to_string(md));  // :1113,1121
+}
+
+void parity_case_w8a8(Iq2MatmulVariant variant) {
+  Case c = parity_inputs();
+  DevCase d = upload(c, Device::hip(0));
+  Tensor y = iq2_matmul_with_activation_quant(d.x, d.wb, d.ws, 7, 320, variant,
+                                              {ActivationQuantMode::W8A8, false});
+  std::vector<float> ref(c.m * c.out_dim);
+  oracle_iq2xxs_matmul_reference_w8a8(c.x.data(), c.m, c.out_dim, c.in_dim, c.wb.data(),
+                                      c.ws.data(), ref.data());
+  const double md = max_abs_diff(y.to_vec<float>(), ref);
+  CHECK(md <= 3e-3, "IQ2 W8A8 parity max_abs too high: " + std::to_string(md));  // :1239,1247
+}
+
+void w8a8_smoke_case(Iq2MatmulVariant variant) {
+  Case c = reference_case(2, 6, 320, 0x0BADC0DE, 0xD15EA5ED, 0xC3);
+  DevCase d = upload(c, Device::hip(0));
+  Tensor y = iq2_matmul_with_activation_quant(d.x, d.wb, d.ws, 6, 320, variant,
+                                              {ActivationQuantMode::W8A8, false});
+  CHECK(y.dims() == (std::vector<size_t>{2, 6}), "shape");
+  for (float v : y.to_vec<float>()) CHECK(std::isfinite(v), "non-finite output");
+}
+
+void cpu_vs_hip_parity_iq2_xxs() { parity_case(Iq2MatmulVariant::Iq2Xxs); }
+void cpu_vs_hip_parity_w8a8_iq2_xxs() { parity_case_w8a8(Iq2MatmulVariant::Iq2Xxs); }
+void w8a8_kernel_smoke_iq2_xxs() { w8a8_smoke_case(Iq2MatmulVariant::Iq2Xxs); }
+
+// The other codebooks are outside this build: the ops fail with a clear error.
+void other_variants_report_not_implemented() {
+  Case c = parity_inputs();
+  DevCase d = upload(c, Device::hip(0));
+  std::vector<uint8_t> big(7 * 2 * 104 + 64, 0), bigs(7 * 2 * 10, 0);
+  Tensor wb = Tensor::from_vec(big, {big.size()}, DType::U8, Device::hip(0));
+  Tensor ws = Tensor::from_vec(bigs, {bigs.size()}, DType::U8, Device::hip(0));
+  for (auto v : {Iq2MatmulVariant::Iq2Xs, Iq2MatmulVariant::Iq2S, Iq2MatmulVariant::Iq3S}) {
+    std::string e = expect_error([&] { iq2_matmul(d.x, wb, ws, 7, 320, v); });
+    CHECK(e.find("not implemented by the ROCm backend") != std::string::npos, e);
+  }
+}
+
+void dequantize_to_f16_bit_exact_iq2_xxs() {
+  Case c = parity_inputs();
+  DevCase d = upload(c, Device::hip(0));
+  Tensor w = iq2_dequantize_to_f16(d.wb, d.ws, 7, 320, Iq2MatmulVariant::Iq2Xxs);
+  CHECK(w.dims() == (std::vector<size_t>{7, 320}) && w.dtype() == DType::F16, "shape/dtype");
+  std::vector<uint16_t> ref(7 * 320);
+  oracle_iq2xxs_dequantize_f16(c.wb.data(), c.ws.data(), 7, 320, ref.data());
+  CHECK(w.to_vec<uint16_t>() == ref, "dequantised f16 differs from the oracle");
+}
+
+void argument_errors_on_device() {
+  Case c = parity_inputs();
+  DevCase d = upload(c, Device::hip(0));
+  Tensor x3 = d.x.reshape({1, 2, 320});
+  std::string e = expect_error([&] { iq2_xxs_matmul(x3, d.wb, d.ws, 7, 320); });
+  CHECK(e == "iq2_matmul expects x rank 1 or 2, got shape [1, 2, 320]", e);
+  e = expect_error([&] { iq2_xxs_matmul(d.x, d.wb, d.ws, 7, 256); });
+  CHECK(e == "iq2_matmul input mismatch: x last dim=320 expected in_dim=256", e);
+  e = expect_error([&] { iq2_xxs_matmul(d.x.narrow(0, 0, 1).reshape({320}), d.wb, d.ws, 7, 300); });
+  CHECK(e == "iq2_matmul input mismatch: x dim=320 expected in_dim=300", e);
+  Tensor short_b = d.wb.narrow(0, 0, 895);
+  e = expect_error([&] { iq2_xxs_matmul(d.x, short_b, d.ws, 7, 320); });
+  CHECK(e == "iq2_matmul weight_bytes too small: got 895 expected at least 896", e);
+  e = expect_error([&] { iq2_xxs_matmul(d.x, d.wb, d.ws.narrow(0, 0, 27), 7, 320); });
+  CHECK(e == "iq2_matmul weight_scales too small: got 27 expected at least 28", e);
+  Tensor wrong = Tensor::from_vec(c.x, {c.x.size()}, DType::F32, Device::hip(0));
+  e = expect_error([&] { iq2_xxs_matmul(d.x, wrong, d.ws, 7, 320); });
+  CHECK(e == "iq2_matmul expects U8 weight bytes/scales, got bytes=F32, scales=U8", e);
+  Tensor xu8 = Tensor::from_vec(std::vector<uint8_t>(640, 1), {2, 320}, DType::U8, Device::hip(0));
+  e = expect_error([&] { iq2_xxs_matmul(xu8, d.wb, d.ws, 7, 320); });
+  CHECK(e == "iq2_matmul unsupported x dtype: U8", e);
+  e = expect_error([&] {
+    iq2_matmul_with_activation_quant(xu8, d.wb, d.ws, 7, 320, Iq2MatmulVariant::Iq2Xxs,
+                                     {ActivationQuantMode::W8A8, false});
+  });
+  CHECK(e == "iq2_matmul_w8a8 unsupported x dtype: U8", e);
+}
+
+void layouts_rank1_strided_and_offset_inputs() {
+  Case c = parity_inputs();
+  DevCase d = upload(c, Device::hip(0));
+  std::vector<float> full = iq2_xxs_matmul(d.x, d.wb, d.ws, 7, 320).to_vec<float>();
+  // rank-1 x gives a rank-1 output equal to the matching row
+  Tensor y1 = iq2_xxs_matmul(d.x.narrow(0, 1, 1).reshape({320}), d.wb, d.ws, 7, 320);
+  CHECK(y1.dims() == (std::vector<size_t>{7}), "rank-1 output shape");
+  std::vector<float> r1 = y1.to_vec<float>();
+  for (size_t i = 0; i < 7; ++i) CHECK(r1[i] == full[7 + i], "rank-1 row differs");
+  // a transposed view of x is made contiguous first
+  std::vector<float> xt(320 * 2);
+  for (size_t r = 0; r < 2; ++r)
+    for (size_t k = 0; k < 320; ++k) xt[k * 2 + r] = c.x[r * 320 + k];
+  Tensor xtv = Tensor::from_vec(xt, {320, 2}, DType::F32, Device::hip(0)).t();
+  CHECK(!xtv.is_contiguous(), "transposed view must be strided");
+  CHECK(iq2_xxs_matmul(xtv, d.wb, d.ws, 7, 320).to_vec<float>() == full, "strided x differs");
+  // weights at a non-zero start offset (layout.start_offset, src/iq2_matmul.rs:320-335),
+  // both 16-byte aligned (fast path) and 1-byte shifted (portable path)
+  for (size_t off : {64u, 1u}) {
+    std::vector<uint8_t> padded(off, 0xEE);
+    padded.insert(padded.end(), c.wb.begin(), c.wb.end());
+    Tensor wbp = Tensor::from_vec(padded, {padded.size()}, DType::U8, Device::hip(0))
+                     .narrow(0, off, c.wb.size());
+    const double md = max_abs_diff(iq2_xxs_matmul(d.x, wbp, d.ws, 7, 320).to_vec<float>(), full);
+    CHECK(md <= 2e-3, "offset weights differ by " + std::to_string(md));
+  }
+  // an empty activation batch returns an empty output
+  Tensor x0 = Tensor::empty({0, 320}, DType::F32, Device::hip(0));
+  Tensor y0 = iq2_xxs_matmul(x0, d.wb, d.ws, 7, 320);
+  CHECK(y0.dims() == (std::vector<size_t>{0, 7}), "empty output shape");
+}
+
+struct Test {
+  const char* name;
+  bool gpu;
+  void (*fn)();
+};
+
+const Test kTests[] = {
+    {"crate_loads", false, crate_loads},
+    {"activation_quant_config_contract", false, activation_quant_config_contract},
+    {"errors_before_any_device_access", false, errors_before_any_device_access},
+    {"cpu_vs_hip_parity_iq2_xxs", true, cpu_vs_hip_parity_iq2_xxs},
+    {"cpu_vs_hip_parity_w8a8_iq2_xxs", true, cpu_vs_hip_parity_w8a8_iq2_xxs},
+    {"w8a8_kernel_smoke_iq2_xxs", true, w8a8_kernel_smoke_iq2_xxs},
+    {"other_variants_report_not_implemented", true, other_variants_report_not_implemented},
+    {"dequantize_to_f16_bit_exact_iq2_xxs", true, dequantize_to_f16_bit_exact_iq2_xxs},
+    {"argument_errors_on_device", true, argument_errors_on_device},
+    {"layouts_rank1_strided_and_offset_inputs", true, layouts_rank1_strided_and_offset_inputs},
+};
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  bool host = false, gpu = false;
+  std::vector<std::string> names;
+  for (int i = 1; i < argc; ++i) {
+    std::string a = argv[i];
+    if (a == "--host") host = true;
+    else if (a == "--gpu") gpu = true;
+    else if (a == "--all") host = gpu = true;
+    else names.push_back(a);
+  }
+  if (!host && !gpu && names.empty()) host = true;
+  int failed = 0, ran = 0;
+  for (const Test& t : kTests) {
+    bool sel = names.empty() ? (t.gpu ? gpu : host) : false;
+    for (const auto& n : names) sel = sel || n == t.name;
+    if (!sel) continue;
+    ++ran;
+    std::printf("test %s ... ", t.name);
+    std::fflush(stdout);
+    try {
+      t.fn();
+      std::printf("ok\n");
+    } catch (const Failure& f) {
+      ++failed;
+      std::printf("FAILED\n    %s\n", f.what.c_str());
+    } catch (const std::exception& e) {
+      ++failed;
+      std::printf("FAILED\n    unexpected exception: %s\n", e.what());
+    }
+    std::fflush(stdout);
+  }
+  std::printf("test result: %s. %d passed; %d failed\n", failed ? "FAILED" : "ok", ran - failed,
+              failed);
+  return failed ? 1 : 0;
+}
