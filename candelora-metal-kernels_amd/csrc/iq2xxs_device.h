@@ -37,6 +37,29 @@ __device__ __forceinline__ uint64_t expand_sign_mask(int i) {
   return v;
 }
 
+// Two-step table fill for kernels with >= 384 threads that want the codebook
+// read issued before their other loads: fetch thread tid's codebook word first
+// (global memory returns in order, so a later wait on it does not wait for
+// loads issued after it), expand it into LDS later.
+__device__ __forceinline__ uint32_t fetch_grid_code(int tid) {
+  return tid < 256 ? kGridCodesDev[tid] : 0u;
+}
+
+__device__ __forceinline__ void store_lds_tables(uint64_t* lds_grid, uint64_t* lds_smask, int tid,
+                                                 uint32_t code) {
+  if (tid < 256) {
+    uint64_t v = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t c = (code >> (2 * j)) & 3u;
+      v |= (uint64_t)(c == 0 ? 8u : (c == 1 ? 25u : 43u)) << (8 * j);
+    }
+    lds_grid[tid] = v;
+  } else if (tid < 384) {
+    lds_smask[tid - 256] = expand_sign_mask(tid - 256);
+  }
+}
+
 // Fill the LDS grid (256 x u64) and sign-mask (128 x u64) tables cooperatively.
 __device__ __forceinline__ void build_lds_tables(uint64_t* lds_grid, uint64_t* lds_smask, int tid,
                                                  int nthreads) {
@@ -46,13 +69,6 @@ __device__ __forceinline__ void build_lds_tables(uint64_t* lds_grid, uint64_t* l
     else
       lds_smask[e - 256] = expand_sign_mask(e - 256);
   }
-}
-
-// Signed int8 weights of one group of 4 columns: magnitudes G (4 bytes) with the
-// bytes selected by M (0xFF) negated.  Per byte: (g ^ 0xFF) + 1 = -g, and since
-// g <= 43 the +1 never carries out of its byte.
-__device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t m) {
-  return (g ^ m) + (m & 0x01010101u);
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
@@ -70,6 +86,73 @@ __device__ __forceinline__ float load_x(const void* x, int dtype, size_t i) {
   return dtype == 1 ? half_bits_to_float(h) : bf16_bits_to_float(h);
 }
 
+// Raw bits of element i of x for a dtype known at compile time (no branches,
+// so the load's result is not waited for until it is used).
+template <int XD>
+__device__ __forceinline__ uint32_t load_x_bits(const void* x, size_t i) {
+  if constexpr (XD == 0)
+    return static_cast<const uint32_t*>(x)[i];
+  else
+    return static_cast<const uint16_t*>(x)[i];
+}
+
+template <int XD>
+__device__ __forceinline__ float x_bits_to_float(uint32_t b) {
+  if constexpr (XD == 0)
+    return __uint_as_float(b);
+  else if constexpr (XD == 1)
+    return half_bits_to_float((uint16_t)b);
+  else
+    return bf16_bits_to_float((uint16_t)b);
+}
+
+// Eight consecutive activations x[base + c0 .. +8) as raw bits, loaded without
+// branches: out-of-range elements read element 0 (always present).  The
+// validity mask is applied in get(), at the point of use, so that no select
+// right after the load forces the wave to wait for it.  kVec: the 8 elements
+// are 16-byte aligned and in_dim % 8 == 0, so they go out as one (16-bit types)
+// or two (f32) 16-byte loads.
+template <int XD, bool kVec>
+struct XOctet {
+  uint32_t raw[kVec && XD != 0 ? 4 : 8];
+  uint32_t okmask;  // bit k: element k is in range
+
+  __device__ __forceinline__ void load(const void* x, size_t base, uint32_t c0, uint32_t in_dim,
+                                       bool valid) {
+    if constexpr (kVec) {
+      const size_t at = valid ? base + c0 : 0;
+      okmask = valid ? 0xFFu : 0u;
+      if constexpr (XD == 0) {
+        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(x) + at);
+        const uint4 a = p[0], b = p[1];
+        raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
+        raw[4] = b.x; raw[5] = b.y; raw[6] = b.z; raw[7] = b.w;
+      } else {
+        const uint4 a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + at);
+        raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
+      }
+    } else {
+      okmask = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const bool ok = valid && c0 + k < in_dim;
+        okmask |= ok ? (1u << k) : 0u;
+        raw[k] = load_x_bits<XD>(x, ok ? base + c0 + k : 0);
+      }
+    }
+  }
+
+  __device__ __forceinline__ float get(int k) const {
+    uint32_t b;
+    if constexpr (kVec && XD != 0)
+      b = (k & 1) ? (raw[k >> 1] >> 16) : (raw[k >> 1] & 0xFFFFu);
+    else
+      b = raw[k];
+    const float v = x_bits_to_float<XD>(b);
+    return ((okmask >> k) & 1u) ? v : 0.0f;
+  }
+};
+
 // W8A8 fake quantisation of one activation (src/metal_src/iq2_matmul.metal:98-102):
 // q = clamp(round_half_away(x * inv), -127, 127); return q / inv.
 __device__ __forceinline__ float qdq_w8a8(float x, float inv_scale) {
@@ -81,22 +164,60 @@ __device__ __forceinline__ float qdq_w8a8(float x, float inv_scale) {
 // ---------------------------------------------------------------------------
 // Activation digits for the int8 MFMA GEMV.
 //
-// A 32-column chunk of fp32 activations with max |x| < 2^e is mapped to
-// integers v = rint(x * 2^(22-e)), |v| <= 2^22.  u = v + 2^23 is a 24-bit
-// unsigned value; its bytes b0,b1,b2 give signed digits s_k = b_k - 128, i.e.
-// the bytes of D = u ^ 0x808080 read as int8.  Then
-//     v = 65536*s2 + 256*s1 + s0 + 32896,   32896 = 128*(65536+256+1) - 2^23,
-// exactly, so sum_k v_k w_k = 65536*C2 + 256*C1 + C0 + 32896*sum_k w_k where
-// C_p = sum_k s_p,k w_k.  The MFMA forms C0..C2 from three digit planes and
-// sum_k w_k from a fourth plane of ones.
-// The chunk scale 2^(e-22) is kept as a float per chunk.
+// A 32-column chunk of activations with max|x| < 2^e is mapped to integers
+// v = rint(x * 2^(21-e)), |v| <= 2^21.  The rounding is one fma against the
+// magic constant 1.5*2^23: the sum's mantissa holds 0x400000 + v exactly.
+// u = v + 0x808080 is a 24-bit unsigned value whose bytes b0,b1,b2 give signed
+// digits s_k = b_k - 128 (the bytes of D = u ^ 0x808080 read as int8) with
+//     v = 65536*s2 + 256*s1 + s0      exactly,
+// so sum_k v_k w_k = 65536*C2 + 256*C1 + C0 with C_p = sum_k s_p,k w_k, the
+// three integer dot products the MFMA forms from three digit planes.
+// The chunk scale 2^(e-21) is kept as a float per chunk.
 // ---------------------------------------------------------------------------
-constexpr int kDigitShift = 22;
-constexpr int kDigitOffset = 32896;  // 128 * (65536 + 256 + 1) - 2^23
+constexpr int kDigitShift = 21;
+constexpr float kDigitMagic = 12582912.0f;       // 1.5 * 2^23
+constexpr uint32_t kDigitBias = 0x4ABF7F80u;     // bits(1.5*2^23) - 0x400000 - 0x808080 + 2^32
 
-__device__ __forceinline__ uint32_t digitize(float x, int e) {
-  int v = __float2int_rn(ldexpf(x, kDigitShift - e));
-  return ((uint32_t)(v + (1 << 23))) ^ 0x808080u;
+// Clamp of the chunk exponent so 2^(21-e) and 2^(e-24) stay finite and normal.
+__device__ __forceinline__ int digit_exponent(float max_abs) {
+  int e;
+  (void)frexpf(max_abs, &e);
+  return e < -100 ? -100 : e;
+}
+
+// Three signed digit bytes (bits 0..23) of x for chunk exponent e.
+__device__ __forceinline__ uint32_t digitize(float x, float scale) {
+  const uint32_t bits = __float_as_uint(fmaf(x, scale, kDigitMagic));
+  return (bits - kDigitBias) ^ 0x808080u;
+}
+
+// Transpose the digit bytes of 4 values into one dword per plane.
+__device__ __forceinline__ void digits_to_planes(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+                                                 uint32_t& p0, uint32_t& p1, uint32_t& p2) {
+  // v_perm_b32(s0, s1, sel): bytes 0-3 of the pool are s1, bytes 4-7 are s0.
+  const uint32_t a = __builtin_amdgcn_perm(d1, d0, 0x05010400u);  // d0.b0 d1.b0 d0.b1 d1.b1
+  const uint32_t b = __builtin_amdgcn_perm(d3, d2, 0x05010400u);  // d2.b0 d3.b0 d2.b1 d3.b1
+  p0 = __builtin_amdgcn_perm(b, a, 0x05040100u);
+  p1 = __builtin_amdgcn_perm(b, a, 0x07060302u);
+  const uint32_t c = __builtin_amdgcn_perm(d1, d0, 0x0c0c0602u);  // d0.b2 d1.b2
+  const uint32_t f = __builtin_amdgcn_perm(d3, d2, 0x0c0c0602u);  // d2.b2 d3.b2
+  p2 = __builtin_amdgcn_perm(f, c, 0x05040100u);
+}
+
+// (g ^ m) + (m & 0x01010101): magnitudes g negated where the byte mask m is 0xFF
+// (per byte (g ^ 0xFF) + 1 = -g; g <= 43 so the +1 never carries).  The
+// compiler selects v_and + v_xad_u32 for it.  Kept in plain C on purpose: the
+// result feeds v_mfma, and only compiler-visible instructions get the
+// VALU-write -> MFMA-read wait states inserted.
+__device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t m) {
+  return (g ^ m) + (m & 0x01010101u);
+}
+
+// 8 * byte G of w: an LDS byte offset into a table of 8-byte entries (the
+// compiler turns the shift-of-a-byte into one SDWA v_lshlrev for G > 0).
+template <int G>
+__device__ __forceinline__ uint32_t byte_times8(uint32_t w) {
+  return ((w >> (8 * G)) & 0xFFu) << 3;
 }
 
 }  // namespace cmk
