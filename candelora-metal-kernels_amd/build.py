@@ -45,6 +45,7 @@ HIP_SOURCES = [
     "iq2xxs_dequant.hip",
     "iq2xxs_gemv.hip",
     "iq2xxs_gemm.hip",
+    "iq2xxs_simple.hip",
     "cmk_iq2.cpp",
 ]
 

@@ -86,10 +86,11 @@ int current_cu_count(int* cus) {
 // Path decision shared by the launch, the workspace query and the path query.
 enum class Path { Gemv, Gemm, Simple };
 
-Path choose_path(int x_dtype, size_t m, uint32_t in_dim, bool wb_aligned16, bool ws_aligned2) {
+Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, bool wb_aligned16,
+                 bool ws_aligned2) {
   const bool half_x = x_dtype == CMK_F16 || x_dtype == CMK_BF16;
   if (half_x && m > kGemvMaxM && ws_aligned2) return Path::Gemm;
-  if (cmk::gemv_supported(in_dim) && wb_aligned16 && ws_aligned2) return Path::Gemv;
+  if (cmk::gemv_supported(out_dim, in_dim) && wb_aligned16 && ws_aligned2) return Path::Gemv;
   return Path::Simple;
 }
 
@@ -177,7 +178,7 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
                            &dims);
   if (rc != CMK_OK) return rc;
   // Assume allocator-aligned buffers (hipMalloc gives 256-byte alignment).
-  Path p = choose_path((int)x_dtype, m, dims.in_dim, true, true);
+  Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, true, true);
   // The simple path can still be chosen at launch for unaligned weights; report
   // the larger need so either choice is covered.
   size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, m);
@@ -188,9 +189,9 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
 
 int cmk_iq2_matmul_path(cmk_dtype x_dtype, size_t m, size_t out_dim, size_t in_dim,
                         cmk_act_quant_mode mode) {
-  (void)out_dim;
   (void)mode;
-  return choose_path((int)x_dtype, m, (uint32_t)(in_dim > UINT32_MAX ? UINT32_MAX : in_dim), true,
+  return choose_path((int)x_dtype, m, (uint32_t)(out_dim > UINT32_MAX ? UINT32_MAX : out_dim),
+                     (uint32_t)(in_dim > UINT32_MAX ? UINT32_MAX : in_dim), true,
                      true) == Path::Gemm
              ? 1
              : 0;
@@ -222,7 +223,7 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul out must be 4-byte aligned");
 
   const bool w8a8 = md == CMK_ACT_QUANT_W8A8;
-  Path p = choose_path((int)x_dtype, m, dims.in_dim, aligned(weight_bytes, 16),
+  Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, aligned(weight_bytes, 16),
                        aligned(weight_scales, 2));
   if (p == Path::Gemm && !aligned(weight_bytes, 8)) p = Path::Simple;
   const size_t need_ws = workspace_for(p, w8a8, m);

@@ -14,17 +14,21 @@ namespace cmk {
 // Per-translation-unit device copy of the codebook codes.
 static __constant__ uint16_t kGridCodesDev[256] = {CMK_IQ2XXS_GRID_CODES};
 
-// Codebook entry e as 8 magnitude bytes (little-endian u64: byte j = weight j).
-__device__ __forceinline__ uint64_t expand_grid_entry(int e) {
-  uint32_t c = kGridCodesDev[e];
+// Codebook entry with level codes `c` (2 bits per byte) as 8 magnitude bytes
+// (little-endian u64: byte j = weight j).
+__device__ __forceinline__ uint64_t grid_entry_from_code(uint32_t c) {
   uint64_t v = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    uint32_t code = (c >> (2 * j)) & 3u;
-    uint32_t lvl = code == 0 ? 8u : (code == 1 ? 25u : 43u);
+    const uint32_t code = (c >> (2 * j)) & 3u;
+    const uint32_t lvl = code == 0 ? 8u : (code == 1 ? 25u : 43u);
     v |= (uint64_t)lvl << (8 * j);
   }
   return v;
+}
+
+__device__ __forceinline__ uint64_t expand_grid_entry(int e) {
+  return grid_entry_from_code(kGridCodesDev[e]);
 }
 
 // Byte mask of the sign pattern ksigns(i): byte j = 0xFF where weight j is negative.
@@ -37,27 +41,11 @@ __device__ __forceinline__ uint64_t expand_sign_mask(int i) {
   return v;
 }
 
-// Two-step table fill for kernels with >= 384 threads that want the codebook
-// read issued before their other loads: fetch thread tid's codebook word first
-// (global memory returns in order, so a later wait on it does not wait for
-// loads issued after it), expand it into LDS later.
-__device__ __forceinline__ uint32_t fetch_grid_code(int tid) {
+// This thread's codebook word (0 for tid >= 256).  Kernels that want the
+// codebook read issued before their other loads fetch it first: global loads
+// return in order, so a later wait on it does not wait for loads issued after.
+__device__ __forceinline__ uint32_t fetch_grid_code(uint32_t tid) {
   return tid < 256 ? kGridCodesDev[tid] : 0u;
-}
-
-__device__ __forceinline__ void store_lds_tables(uint64_t* lds_grid, uint64_t* lds_smask, int tid,
-                                                 uint32_t code) {
-  if (tid < 256) {
-    uint64_t v = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t c = (code >> (2 * j)) & 3u;
-      v |= (uint64_t)(c == 0 ? 8u : (c == 1 ? 25u : 43u)) << (8 * j);
-    }
-    lds_grid[tid] = v;
-  } else if (tid < 384) {
-    lds_smask[tid - 256] = expand_sign_mask(tid - 256);
-  }
 }
 
 // Fill the LDS grid (256 x u64) and sign-mask (128 x u64) tables cooperatively.
@@ -106,12 +94,13 @@ __device__ __forceinline__ float x_bits_to_float(uint32_t b) {
     return bf16_bits_to_float((uint16_t)b);
 }
 
-// Eight consecutive activations x[base + c0 .. +8) as raw bits, loaded without
-// branches: out-of-range elements read element 0 (always present).  The
-// validity mask is applied in get(), at the point of use, so that no select
-// right after the load forces the wave to wait for it.  kVec: the 8 elements
-// are 16-byte aligned and in_dim % 8 == 0, so they go out as one (16-bit types)
-// or two (f32) 16-byte loads.
+// Eight consecutive activations x[base + c0 .. +8) as raw bits.  A task that
+// is out of range issues no load at all (its registers stay undefined) and
+// in-range elements are never selected right after the load: the validity
+// mask is applied in get(), at the point of use, so that nothing forces the
+// wave to wait for the load early.  kVec: the 8 elements are 16-byte aligned
+// and in_dim % 8 == 0, so they go out as one (16-bit types) or two (f32)
+// 16-byte loads.
 template <int XD, bool kVec>
 struct XOctet {
   uint32_t raw[kVec && XD != 0 ? 4 : 8];
@@ -120,16 +109,18 @@ struct XOctet {
   __device__ __forceinline__ void load(const void* x, size_t base, uint32_t c0, uint32_t in_dim,
                                        bool valid) {
     if constexpr (kVec) {
-      const size_t at = valid ? base + c0 : 0;
       okmask = valid ? 0xFFu : 0u;
-      if constexpr (XD == 0) {
-        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(x) + at);
-        const uint4 a = p[0], b = p[1];
-        raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
-        raw[4] = b.x; raw[5] = b.y; raw[6] = b.z; raw[7] = b.w;
-      } else {
-        const uint4 a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + at);
-        raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
+      if (valid) {
+        if constexpr (XD == 0) {
+          const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(x) + base + c0);
+          const uint4 a = p[0], b = p[1];
+          raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
+          raw[4] = b.x; raw[5] = b.y; raw[6] = b.z; raw[7] = b.w;
+        } else {
+          const uint4 a =
+              *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + c0);
+          raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
+        }
       }
     } else {
       okmask = 0;
@@ -137,9 +128,16 @@ struct XOctet {
       for (int k = 0; k < 8; ++k) {
         const bool ok = valid && c0 + k < in_dim;
         okmask |= ok ? (1u << k) : 0u;
-        raw[k] = load_x_bits<XD>(x, ok ? base + c0 + k : 0);
+        if (ok) raw[k] = load_x_bits<XD>(x, base + c0 + k);
       }
     }
+  }
+
+  // Blocks until the loads of this octet have returned (an empty asm that
+  // reads the registers; the compiler places the wait in front of it).
+  __device__ __forceinline__ void wait_arrived() const {
+#pragma unroll
+    for (int k = 0; k < (int)(sizeof(raw) / sizeof(raw[0])); ++k) asm volatile("" ::"v"(raw[k]));
   }
 
   __device__ __forceinline__ float get(int k) const {
@@ -211,13 +209,6 @@ __device__ __forceinline__ void digits_to_planes(uint32_t d0, uint32_t d1, uint3
 // VALU-write -> MFMA-read wait states inserted.
 __device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t m) {
   return (g ^ m) + (m & 0x01010101u);
-}
-
-// 8 * byte G of w: an LDS byte offset into a table of 8-byte entries (the
-// compiler turns the shift-of-a-byte into one SDWA v_lshlrev for G > 0).
-template <int G>
-__device__ __forceinline__ uint32_t byte_times8(uint32_t w) {
-  return ((w >> (8 * G)) & 0xFFu) << 3;
 }
 
 }  // namespace cmk
