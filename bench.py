@@ -304,7 +304,7 @@ def main():
         "frac_of_hbm_peak": value / HBM_PEAK_GBS,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "cmk::iq2xxs_gemv_kernel<2>",
+                     "kernel": "cmk::iq2xxs_gemv_kernel<0, true>",
                      "mean_launch_us": dec["mean_launch_us"],
                      "alg_bytes_per_launch": dec["per_launch_bytes"]},
     }
