@@ -90,7 +90,9 @@ Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, bool 
                  bool ws_aligned2) {
   const bool half_x = x_dtype == CMK_F16 || x_dtype == CMK_BF16;
   if (half_x && m > kGemvMaxM && ws_aligned2) return Path::Gemm;
-  if (cmk::gemv_supported(out_dim, in_dim) && wb_aligned16 && ws_aligned2) return Path::Gemv;
+  if (m <= UINT32_MAX && cmk::gemv_supported((uint32_t)m, out_dim, in_dim, x_dtype) &&
+      wb_aligned16 && ws_aligned2)
+    return Path::Gemv;
   return Path::Simple;
 }
 

@@ -5,27 +5,44 @@
 // output walking all of K serially with byte loads, and (for W8A8) rescan the
 // whole x row per thread to find its max.
 //
-// Design (one launch, no scratch memory, one workgroup of up to 16 waves per
-// CU for the usual shapes):
-//  * Activations are turned into exact integer digits once per workgroup:
-//    each 32-column chunk with max|x| < 2^e becomes v = rint(x*2^(21-e)) split
-//    into three signed 8-bit digit planes (iq2xxs_device.h), held in LDS.
-//  * The weights stream from HBM with 16-byte buffer loads, one pair of
-//    32-weight sub-blocks per lane and row group.  Absent rows and pairs get an
-//    offset past the buffer's size, so they read zeros without touching memory
-//    and without a branch.
-//  * Codes expand through two LDS tables (codebook bytes, sign byte-masks)
-//    replicated 16 times: lane l reads copy l & 15, so the 16 lanes the LDS
-//    serves together hit 16 different bank pairs whatever entries they ask for.
-//    One v_perm forms each table address from a code byte.
-//  * v_mfma_i32_4x4x4_16b_i8 does the dot products: in each of the 16 4x4
-//    blocks, the A rows are the three digit planes (the fourth row is zero),
-//    the B columns are 4 weight rows, so eight instructions give, for 4 rows,
-//    the three digit sums of a 32-column sub-block.  The sub-block scale
-//    d*(2s+1)/8 * 2^(e-21) is applied in fp32 when the sums are folded in.
-//  * Each wave reduces its 16 blocks with a fixed butterfly; the workgroup
-//    then adds the K-slices of a row in slice order.  Results are
-//    deterministic.
+// Work split.  One workgroup of 16 waves per CU.  A workgroup owns a chunk of
+// consecutive 4-row groups; a *tile* is one row group x 16 sub-block pairs
+// (1024 columns), i.e. one 16-byte weight load per lane.  Tiles are numbered
+// slice-major (tile = slice * n_rg + rg) and each wave takes a contiguous run
+// of them, so a wave mostly reuses one slice of activation digits, and the
+// tile counts of the 4 waves that share a SIMD differ by at most one.
+//
+// Arithmetic.
+//  * Activations become exact integer digits: each 32-column chunk with
+//    max|x| < 2^e gives v = rint(x*2^(21-e)) split into three signed 8-bit
+//    digit planes (iq2xxs_device.h), held in LDS.
+//  * Codes expand through two LDS tables: a codebook row holds 16 copies of
+//    {g, -g} (8 magnitude bytes and their negations), a sign row 32 copies of
+//    the 8-byte sign mask; lane l reads copy l & 15 (resp. l & 31), so every
+//    read is free of bank conflicts.  One v_bitop3 (bit select) per dword
+//    picks g or -g under the mask.
+//  * v_mfma_i32_4x4x4_16b_i8: in each of the 16 4x4 blocks the A rows are the
+//    three digit planes (the fourth row is zero) and the B columns are 4 weight
+//    rows; eight instructions give, for 4 rows, the three digit sums of a
+//    32-column sub-block.  The scale d*(2s+1)/8 * 2^(e-21) is applied in fp32.
+//  * A wave sums its 16 blocks with DPP and lane-swap moves; the workgroup
+//    adds the slices of a row in slice order.  Results are deterministic.
+//
+// Schedule.  A CU's memory pipeline serves requests roughly in issue order and
+// a wave that issues a load stalls while the pipeline is full, so the order of
+// issue matters:
+//   1. every wave issues its set-up loads (codebook word, the chunk's scales,
+//      its share of the activation row) and the workgroup meets at a barrier,
+//      so those loads are ahead of every weight load;
+//   2. every wave issues its first two weight tiles;
+//   3. waves 0-7 build the tables, waves 15, 14, ... digitise, everyone stages
+//      the scales; barrier;
+//   4. each wave issues tile k+2 and computes tile k.
+// All waves run the same code with the same sequence of loads, so the
+// compiler's count of outstanding loads (s_waitcnt vmcnt) is exact: a wave
+// waits for exactly the load it is about to use.  The first chunk and row are
+// straight-line code for the same reason; further rows (m > 1) and chunks
+// (large out_dim) loop behind it.
 //
 // Bound: HBM.  Algorithmic bytes per weight row: ceil(K/256)*66, plus x and
 // out once.
@@ -47,88 +64,167 @@ __device__ __forceinline__ v4i mfma4x4(int a_xdigits, int b_weights, v4i c) {
   return __builtin_amdgcn_mfma_i32_4x4x4i8(a_xdigits, b_weights, c, 0, 0, 0);
 }
 
-constexpr uint32_t kGemvMaxWaves = 16;
-constexpr uint32_t kGemvT = 2;     // sub-block pairs per lane per row group
-constexpr uint32_t kGemvMaxR = 2;  // row groups per wave (weights held in registers)
-// Digitisation tasks per thread whose activations are loaded before the
-// weights (more would spill at 128 VGPRs).
-template <bool kVecX>
-constexpr uint32_t gemv_max_xt() {
-  return kVecX ? 2 : 1;
-}
+constexpr uint32_t kGemvWaves = 16;
+constexpr uint32_t kGemvThreads = kGemvWaves * 64;
+constexpr uint32_t kSlicePairs = 16;   // sub-block pairs per tile (one per 4x4 block)
+constexpr uint32_t kTilesPerWave = 4;  // weight tiles a wave holds
+constexpr uint32_t kTilesAhead = 2;    // tiles in flight ahead of the one computed
+constexpr uint32_t kScaleLoads = 2;    // staged scales per thread and chunk
 constexpr uint32_t kGemvLdsLimit = 160 * 1024;
-// Buffer offset past every num_records used here (weights are < 2^31 bytes).
+// Buffer offset past every num_records used here (buffers are < 2^31 bytes).
 constexpr uint32_t kOutOfRange = 0x80000000u;
 // Word 3 of a gfx9 raw buffer resource (32-bit data format, no swizzle).
 constexpr int kBufferWord3 = 0x00020000;
 
-// Replicated lookup tables at LDS offset 0: row r (0..255) is 256 bytes;
-// bytes [0, 128) hold 16 copies of codebook entry r (8 magnitude bytes each),
-// bytes [128, 256) hold 16 copies of the sign byte-mask of ksigns(r & 127).
-constexpr uint32_t kTableRowBytes = 256;
-constexpr uint32_t kTableBytes = 256 * kTableRowBytes;
-constexpr uint32_t kSignHalf = 128;
+// Table layouts at LDS offset 0.
+//  wide:   [0, 64K)   codebook row e (256 B) = 16 copies of {g lo, g hi, -g lo, -g hi}
+//          [64K, 96K) sign row i (256 B) = 32 copies of the 8-byte mask of ksigns(i)
+//  narrow: [0, 64K)   row r (256 B): bytes [0,128) 8 codebook copies of entry r,
+//          bytes [128, 256) 16 copies of the sign mask of ksigns(r & 127); the
+//          sign index then needs no masking (a byte of aux_s << g carries one
+//          unrelated bit on top), at the price of 2-way bank conflicts.
+template <bool kWide>
+struct GemvTables {
+  static constexpr uint32_t kBytes = kWide ? 96 * 1024 : 64 * 1024;
+  static constexpr uint32_t kGridCopies = kWide ? 16 : 8;
+  static constexpr uint32_t kSignCopies = kWide ? 32 : 16;
+  static constexpr uint32_t kSignBase = kWide ? 65536 : 128;
+};
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
                                            kBufferWord3);
 }
 
-// Fill the replicated tables.  Slot u < 256 is codebook row u, slot 256 + i
-// the sign row i (rows 128..255 repeat rows 0..127: a sign index read as a
-// byte carries one unrelated bit on top).  Lane-rotated copy order keeps the
-// 16 stores of a lane group on distinct banks.
-__device__ __forceinline__ void store_table_slot(uint8_t* lds, uint32_t u, uint64_t v) {
-  const uint32_t base = (u & 255) * kTableRowBytes + (u >> 8) * kSignHalf;
-#pragma unroll
-  for (uint32_t k = 0; k < 16; ++k)
-    *reinterpret_cast<uint64_t*>(lds + base + 8 * ((u + k) & 15)) = v;
+// All copies of codebook row e; the copy order is rotated by e so the 16
+// lanes the LDS serves together write 16 different bank groups.
+template <bool kWide>
+__device__ __forceinline__ void store_grid_row(uint8_t* lds, uint32_t e, uint64_t g) {
+  const uint32_t lo = (uint32_t)g, hi = (uint32_t)(g >> 32);
+  // per-byte negation: (~g) + 1 never carries across bytes since g >= 8
+  const u32x4 v = {lo, hi, ~lo + 0x01010101u, ~hi + 0x01010101u};
+  constexpr uint32_t C = GemvTables<kWide>::kGridCopies;
+#pragma unroll 2
+  for (uint32_t k = 0; k < C; ++k)
+    *reinterpret_cast<u32x4*>(lds + e * 256 + 16 * ((k + e) & (C - 1))) = v;
 }
 
-// `code_tid` is this thread's codebook word, fetched before the weight loads
-// were issued; only workgroups of fewer than 512 threads load more words here
-// (in a separate loop, so the first slot never waits for the weights).
-__device__ __forceinline__ void build_replicated_tables(uint8_t* lds, uint32_t tid,
-                                                        uint32_t nthreads, uint32_t code_tid) {
-  if (tid < 512)
-    store_table_slot(lds, tid,
-                     tid < 256 ? grid_entry_from_code(code_tid) : expand_sign_mask((int)(tid & 127)));
-  for (uint32_t u = tid + nthreads; u < 512; u += nthreads)
-    store_table_slot(lds, u, u < 256 ? expand_grid_entry((int)u) : expand_sign_mask((int)(u & 127)));
+// Copies [k0, k0 + n) of sign row i (rotated like the codebook rows).
+template <bool kWide>
+__device__ __forceinline__ void store_sign_row(uint8_t* lds, uint32_t i, uint64_t m, uint32_t k0,
+                                               uint32_t n) {
+  const u32x2 v = {(uint32_t)m, (uint32_t)(m >> 32)};
+  constexpr uint32_t C = GemvTables<kWide>::kSignCopies;
+#pragma unroll 2
+  for (uint32_t k = k0; k < k0 + n; ++k)
+    *reinterpret_cast<u32x2*>(lds + GemvTables<kWide>::kSignBase + i * 256 +
+                              8 * ((k + i) & (C - 1))) = v;
 }
 
 // Table address  256 * byte G of w + low byte of cbase  as one v_perm
 // (result bytes: cbase.b0, w.bG, 0, 0).
 template <int G>
-__device__ __forceinline__ uint32_t table_addr(uint32_t w, uint32_t cbase) {
+__device__ __forceinline__ uint32_t perm_addr(uint32_t w, uint32_t cbase) {
   return __builtin_amdgcn_perm(w, cbase, 0x0C0C0000u | ((0x04u + G) << 8));
 }
 
-// 8-byte LDS read at a byte address (the kernel's dynamic LDS starts at 0).
-__device__ __forceinline__ u32x2 lds_load_u2(uint32_t addr) {
+// Sign-row address of group G of aux_s for this lane's copy base cs.
+template <bool kWide, int G>
+__device__ __forceinline__ uint32_t sign_addr(uint32_t aux_s, uint32_t cs) {
+  if constexpr (kWide)
+    return (__builtin_amdgcn_ubfe(aux_s, 7 * G, 7) << 8) | cs;
+  else
+    return perm_addr<G>(aux_s << G, cs);
+}
+
+// LDS reads at byte addresses (the kernel's dynamic LDS starts at 0).
+__device__ __forceinline__ u32x2 lds_u2(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
       static_cast<uintptr_t>(addr));
 }
-
-// Makes v look modified here (emits no instruction).  Used on the weight
-// registers right before they are decoded, so the decode's address arithmetic
-// cannot be hoisted out of the activation-row loop, where it would wait for
-// every weight load and hold all addresses in registers at once.
-// The scale stays a 16-bit value until then: widening it would be hoisted too
-// (v_cvt_f32_f16 reads only the low half of the register anyway).
-__device__ __forceinline__ void pin_here(u32x4& v, uint16_t& d) {
-  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w), "+v"(d));
+__device__ __forceinline__ u32x4 lds_u4(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+      static_cast<uintptr_t>(addr));
 }
 
-// Sum of v over the 16 lanes of a wave that share lane & 3, in a fixed order.
+// Bits of a where m is set, of b elsewhere (one v_bitop3 on gfx950).  Kept in
+// plain C: the result feeds v_mfma, and only compiler-visible instructions
+// get the VALU-write -> MFMA-read wait states inserted.
+__device__ __forceinline__ uint32_t bit_select(uint32_t m, uint32_t a, uint32_t b) {
+  return (m & a) | (~m & b);
+}
+
+// Makes v look modified here (emits no instruction): the decode of a tile's
+// codes cannot be hoisted out of the activation-row loop (m > 1), where it
+// would hold every decoded tile in registers at once.
+__device__ __forceinline__ void pin_here(u32x4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+
+// Sum over the 16 lanes that share lane & 3 (the 16 4x4 blocks), in a fixed
+// order, with VALU lane moves only.
 __device__ __forceinline__ float sum_over_blocks(float v) {
-  // row_ror:4 and row_ror:8 inside each 16-lane row, then across rows.
+  // row_ror:4 and row_ror:8 inside each 16-lane row
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  // then across rows: lanes l and l ^ 16, then l and l ^ 32
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
+
+// Max over the 4 lanes of an aligned quad (DPP quad_perm [1,0,3,2], [2,3,0,1]).
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF,
+                                                          false)));
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF,
+                                                             false)));
+}
+
+// Eight consecutive activations (one digitisation task) by buffer loads.  An
+// absent task or element reads at an offset past the buffer and gets zeros,
+// with no branch, so the count of outstanding loads is the same on every path.
+// kVec: the 8 elements are 16-byte aligned and in_dim % 8 == 0.
+template <int XD, bool kVec>
+struct XTask {
+  static constexpr uint32_t kRegs = (kVec && XD != 0) ? 4 : 8;
+  uint32_t raw[kRegs];
+
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rx, uint32_t elem0, uint32_t c0,
+                                       uint32_t in_dim, bool valid) {
+    constexpr uint32_t es = XD == 0 ? 4 : 2;
+    if constexpr (kVec) {
+      const uint32_t off = valid ? elem0 * es : kOutOfRange;
+      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+      raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
+      if constexpr (XD == 0) {
+        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16, 0, 0);
+        raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
+      }
+    } else {
+#pragma unroll
+      for (uint32_t k = 0; k < 8; ++k) {
+        const uint32_t off = (valid && c0 + k < in_dim) ? (elem0 + k) * es : kOutOfRange;
+        if constexpr (XD == 0)
+          raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0);
+        else
+          raw[k] = __builtin_amdgcn_raw_buffer_load_b16(rx, off, 0, 0);
+      }
+    }
+  }
+
+  __device__ __forceinline__ float get(int k) const {
+    uint32_t b;
+    if constexpr (kVec && XD != 0)
+      b = (k & 1) ? (raw[k >> 1] >> 16) : (raw[k >> 1] & 0xFFFFu);
+    else
+      b = raw[k];
+    return x_bits_to_float<XD>(b);
+  }
+};
 
 struct GemvArgs {
   const void* x;
@@ -138,284 +234,330 @@ struct GemvArgs {
   uint32_t m, out_dim, in_dim;
   uint32_t bpr;           // super-blocks per row
   uint32_t npairs;        // sub-block pairs per row = 4 * bpr
-  uint32_t slices;        // waves that split one row group's K range
-  uint32_t teams;         // wave groups; team t takes row groups t, t + teams, ...
-  uint32_t rgs;           // row groups per wave (<= kGemvMaxR)
-  uint32_t rg_per_wg;     // teams * rgs
-  uint32_t xt;            // digitisation tasks per thread per round (<= gemv_max_xt)
-  uint32_t wb_records;    // bytes of weight_bytes covering out_dim rows
-  uint32_t ws_records;    // bytes of weight_scales covering out_dim rows
+  uint32_t nslices;       // tiles per row group = ceil(npairs / 16)
+  uint32_t rg_per_chunk;  // row groups per chunk
+  uint32_t nchunks;
+  uint32_t ntasks;        // digitisation tasks per activation row (8 columns each)
+  uint32_t wb_records, ws_records, x_records;  // bytes addressable by the buffer loads
   uint32_t plane_stride;  // LDS bytes between the three digit planes
+  uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs;  // LDS layout
   int w8a8;
 };
 
-// LDS layout (dynamic): tables (64 KB) | xsc[2*npairs] f32 |
-//   xdig[3][plane_stride] | red[rg_per_wg][slices][4] f32 | wave maxima[16] f32
 // XD: activation dtype (0 f32, 1 f16, 2 bf16); kVecX: activations can be read
-// as aligned 16-byte vectors.  All global loads are branch-free, so the
-// compiler waits for a load only where its value is used, and loads complete
-// in issue order: activations first, then weights.
-template <int XD, bool kVecX>
-__global__ __launch_bounds__(kGemvMaxWaves * 64) void iq2xxs_gemv_kernel(GemvArgs a) {
+// as aligned 16-byte vectors; kWide: table layout; kXT: digitisation tasks
+// per thread per round; kW8A8: fake-quantise x per row first; kMulti: m > 1 or
+// more than one chunk per workgroup (the loops are compiled out otherwise).
+template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti>
+__global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
-  const uint32_t nsb = a.npairs * 2;
-  float* xsc = reinterpret_cast<float*>(lds + kTableBytes);
-  uint8_t* xdig = reinterpret_cast<uint8_t*>(xsc + nsb);
-  float* red = reinterpret_cast<float*>(xdig + 3 * a.plane_stride);
-  float* s_wred = red + a.rg_per_wg * a.slices * 4;
+  using TL = GemvTables<kWide>;
+  uint16_t* sscale = reinterpret_cast<uint16_t*>(lds + a.scale_ofs);
+  float* xsc = reinterpret_cast<float*>(lds + a.xsc_ofs);
+  uint8_t* xdig = lds + a.xdig_ofs;
+  float* red = reinterpret_cast<float*>(lds + a.red_ofs);
+  float* s_wred = reinterpret_cast<float*>(lds + a.wred_ofs);
 
-  const uint32_t nthreads = blockDim.x;
-  const uint32_t nwaves = nthreads >> 6;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t b = lane >> 2;  // 4x4 block within the wave
-  const uint32_t j = lane & 3;   // row of the 4-row group / digit plane of this lane
-  const uint32_t slice = wave % a.slices;
-  const uint32_t team = wave / a.slices;
-
-  const uint32_t rg_begin = blockIdx.x * a.rg_per_wg;
+  const uint32_t rtid = kGemvThreads - 1 - tid;  // digitisation order: last waves first
+  const uint32_t b = lane >> 2;                  // 4x4 block of this lane
+  const uint32_t j = lane & 3;                   // row in the row group / digit plane
   const uint32_t n_rg_total = (a.out_dim + 3) / 4;
-  const uint32_t rg_end = min(rg_begin + a.rg_per_wg, n_rg_total);
-  const uint32_t ntasks = nsb * 4;
-  constexpr uint32_t kMaxXT = gemv_max_xt<kVecX>();
+  const uint32_t row_bytes = a.bpr * kBytesPerBlock;
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, a.x_records);
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.wb, a.wb_records);
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.ws, a.ws_records);
+  const uint32_t round = kGemvThreads * kXT;  // tasks per digitisation round
 
-  // ---- Order of work.  The weight stream of all CUs fills the memory
-  // queues for microseconds; a request issued behind it waits that long, and
-  // a wave whose weight loads back up in its CU's memory pipeline stalls at
-  // issue.  So everything that needs no weights comes first: the codebook
-  // word and the activations of row 0 are loaded, the tables are built and
-  // the activations digitised, and only then are the weights issued.
-  const uint32_t grid_code = fetch_grid_code(tid);
-  XOctet<XD, kVecX> xo[kMaxXT];
-  auto load_x_tasks = [&](uint32_t task0, size_t xbase) {
+  // ---- chunk geometry and this wave's tiles
+  uint32_t chunk = blockIdx.x;
+  uint32_t row_begin, n_rg, rows, t0, cnt;
+  auto set_chunk = [&](uint32_t c) {
+    const uint32_t rg_begin = c * a.rg_per_chunk;
+    const uint32_t rg_end = min(rg_begin + a.rg_per_chunk, n_rg_total);
+    n_rg = rg_end - rg_begin;
+    row_begin = rg_begin * 4;
+    rows = min(rg_end * 4, a.out_dim) - row_begin;
+    const uint32_t ntiles = n_rg * a.nslices;
+    const uint32_t base = ntiles / kGemvWaves, extra = ntiles - base * kGemvWaves;
+    cnt = base + (wave < extra ? 1u : 0u);
+    t0 = wave * base + min(wave, extra);
+  };
+  auto load_tile = [&](uint32_t k) -> u32x4 {
+    const uint32_t tau = t0 + k;
+    const uint32_t slice = tau / n_rg;
+    const uint32_t rgl = tau - slice * n_rg;
+    const uint32_t row = row_begin + rgl * 4 + j;
+    const uint32_t pair = slice * kSlicePairs + b;
+    const bool ok = k < cnt && row < a.out_dim && pair < a.npairs;
+    return __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? row * row_bytes + pair * 16 : kOutOfRange,
+                                                 0, 0);
+  };
+  uint32_t sraw[kScaleLoads];
+  auto load_scales = [&]() {
+    const uint32_t nscales = rows * a.bpr;
 #pragma unroll
-    for (uint32_t u = 0; u < kMaxXT; ++u) {
-      if (u >= a.xt) break;  // uniform
-      const uint32_t task = task0 + tid + u * nthreads;
+    for (uint32_t k = 0; k < kScaleLoads; ++k) {
+      const uint32_t i = tid + k * kGemvThreads;
+      sraw[k] = __builtin_amdgcn_raw_buffer_load_b16(
+          rs, i < nscales ? (row_begin * a.bpr + i) * kScalesPerBlock : kOutOfRange, 0, 0);
+    }
+  };
+  auto stage_scales = [&]() {
+    const uint32_t nscales = rows * a.bpr;
+#pragma unroll
+    for (uint32_t k = 0; k < kScaleLoads; ++k) {
+      const uint32_t i = tid + k * kGemvThreads;
+      if (i < nscales) sscale[i] = (uint16_t)sraw[k];
+    }
+  };
+
+  // ---- activation digits
+  XTask<XD, kVecX> xo[kXT];
+  auto load_x = [&](uint32_t r0, uint32_t mrow) {
+#pragma unroll
+    for (uint32_t u = 0; u < (uint32_t)kXT; ++u) {
+      const uint32_t task = r0 + u * kGemvThreads + rtid;
       const uint32_t c0 = (task >> 2) * 32 + (task & 3) * 8;
-      xo[u].load(a.x, xbase, c0, a.in_dim, task < ntasks && c0 < a.in_dim);
+      xo[u].load(rx, mrow * a.in_dim + c0, c0, a.in_dim, task < a.ntasks && c0 < a.in_dim);
     }
   };
-
-  // Digit planes of activation row `mrow` into xdig / xsc: 4 threads per
-  // 32-column chunk, 8 columns each.  The first round of activations must
-  // already be in xo.
+  // W8A8 row scale (iq2_matmul.metal:86-96) from the row's values in xo (the
+  // row fits in one round) or by a second pass over the row; ends in a barrier.
+  auto w8a8_inv_scale = [&](uint32_t mrow) -> float {
+    float mx = 0.0f;
+    if (a.ntasks <= round) {
+#pragma unroll
+      for (uint32_t u = 0; u < (uint32_t)kXT; ++u)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(xo[u].get(k)));
+    } else {
+      const size_t xbase = (size_t)mrow * a.in_dim;
+      for (uint32_t c = tid; c < a.in_dim; c += kGemvThreads)
+        mx = fmaxf(mx, fabsf(x_bits_to_float<XD>(load_x_bits<XD>(a.x, xbase + c))));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) s_wred[wave] = mx;
+    __syncthreads();
+    mx = 0.0f;
+#pragma unroll
+    for (uint32_t w = 0; w < kGemvWaves; ++w) mx = fmaxf(mx, s_wred[w]);
+    return (mx < 1e-8f) ? 1.0f : 127.0f / mx;
+  };
+  // Digits of the round of tasks held in xo: 4 threads per 32-column chunk
+  // (an aligned quad of lanes), 8 columns each.
+  auto digitize_round = [&](uint32_t r0, float inv_scale) {
+#pragma unroll
+    for (uint32_t u = 0; u < (uint32_t)kXT; ++u) {
+      const uint32_t task = r0 + u * kGemvThreads + rtid;
+      float xv[8];
+      float mx = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        xv[k] = xo[u].get(k);
+        if constexpr (kW8A8) xv[k] = qdq_w8a8(xv[k], inv_scale);
+        mx = fmaxf(mx, fabsf(xv[k]));
+      }
+      mx = quad_max(mx);
+      if (task < a.ntasks) {
+        const int e = digit_exponent(mx);
+        const float scale = ldexpf(1.0f, kDigitShift - e);
+        uint32_t dg[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dg[k] = digitize(xv[k], scale);
+        uint32_t p0[2], p1[2], p2[2];
+        digits_to_planes(dg[0], dg[1], dg[2], dg[3], p0[0], p1[0], p2[0]);
+        digits_to_planes(dg[4], dg[5], dg[6], dg[7], p0[1], p1[1], p2[1]);
+        const uint32_t c0 = (task >> 2) * 32 + (task & 3) * 8;
+        *reinterpret_cast<uint2*>(xdig + c0) = make_uint2(p0[0], p0[1]);
+        *reinterpret_cast<uint2*>(xdig + a.plane_stride + c0) = make_uint2(p1[0], p1[1]);
+        *reinterpret_cast<uint2*>(xdig + 2 * a.plane_stride + c0) = make_uint2(p2[0], p2[1]);
+        if ((task & 3) == 0) xsc[task >> 2] = ldexpf(1.0f, e - kDigitShift - 3);
+      }
+    }
+  };
+  // Digits of row mrow whose first round is in xo; rounds beyond the first
+  // (in_dim > 8192 * kXT) load behind the first weight tiles.
   auto digitize_row = [&](uint32_t mrow) {
-    const size_t xbase = (size_t)mrow * a.in_dim;
-    // W8A8 row scale (iq2_matmul.metal:86-96), reduced over the whole row.
     float inv_scale = 1.0f;
-    if (a.w8a8) {
-      float mx0 = 0.0f, mx1 = 0.0f;
-      for (uint32_t c = tid; c < a.in_dim; c += 2 * nthreads) {
-        const uint32_t c1 = c + nthreads;
-        const uint32_t b0 = load_x_bits<XD>(a.x, xbase + c);
-        const uint32_t b1 = load_x_bits<XD>(a.x, c1 < a.in_dim ? xbase + c1 : xbase);
-        mx0 = fmaxf(mx0, fabsf(x_bits_to_float<XD>(b0)));
-        mx1 = fmaxf(mx1, fabsf(x_bits_to_float<XD>(b1)));
-      }
-      float mx = fmaxf(mx0, mx1);
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-      if (lane == 0) s_wred[wave] = mx;
-      __syncthreads();
-      mx = 0.0f;
-      for (uint32_t w = 0; w < nwaves; ++w) mx = fmaxf(mx, s_wred[w]);
-      inv_scale = (mx < 1e-8f) ? 1.0f : 127.0f / mx;
-    }
-    const uint32_t round = nthreads * a.xt;
-    for (uint32_t task0 = 0; task0 < ntasks; task0 += round) {
-      if (task0 > 0) load_x_tasks(task0, xbase);  // activations beyond the first round
-#pragma unroll
-      for (uint32_t u = 0; u < kMaxXT; ++u) {
-        // the 4 tasks of a chunk sit in 4 consecutive lanes: all active or none
-        if (u >= a.xt || task0 + u * nthreads >= ntasks) break;
-        const uint32_t task = task0 + tid + u * nthreads;
-        float xv[8];
-        float mx = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          xv[k] = xo[u].get(k);
-          if (a.w8a8) xv[k] = qdq_w8a8(xv[k], inv_scale);
-          mx = fmaxf(mx, fabsf(xv[k]));
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
-        if (task < ntasks) {
-          const int e = digit_exponent(mx);
-          const float scale = ldexpf(1.0f, kDigitShift - e);
-          uint32_t dg[8];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) dg[k] = digitize(xv[k], scale);
-          uint32_t p0[2], p1[2], p2[2];
-          digits_to_planes(dg[0], dg[1], dg[2], dg[3], p0[0], p1[0], p2[0]);
-          digits_to_planes(dg[4], dg[5], dg[6], dg[7], p0[1], p1[1], p2[1]);
-          const uint32_t c0 = (task >> 2) * 32 + (task & 3) * 8;
-          *reinterpret_cast<uint2*>(xdig + c0) = make_uint2(p0[0], p0[1]);
-          *reinterpret_cast<uint2*>(xdig + a.plane_stride + c0) = make_uint2(p1[0], p1[1]);
-          *reinterpret_cast<uint2*>(xdig + 2 * a.plane_stride + c0) = make_uint2(p2[0], p2[1]);
-          if ((task & 3) == 0) xsc[task >> 2] = ldexpf(1.0f, e - kDigitShift - 3);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // one task at a time: bounds register use
-      }
+    if constexpr (kW8A8) inv_scale = w8a8_inv_scale(mrow);
+    digitize_round(0, inv_scale);
+    for (uint32_t r0 = round; r0 < a.ntasks; r0 += round) {
+      load_x(r0, mrow);
+      digitize_round(r0, inv_scale);
     }
   };
-
-  // The digit planes are complete once every wave has passed this barrier.
-  // The scheduler is fenced on both sides: weight-dependent work hoisted
-  // above it would make every wave wait for its weights here.
-  auto digits_ready = [&]() {
+  auto sync = [&]() {
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  load_x_tasks(0, 0);
-  build_replicated_tables(lds, tid, nthreads, grid_code);
-  digitize_row(0);
-  digits_ready();
-  // Each wave issues its weights only now and then works on them as they
-  // arrive: no barrier stands between a wave's loads and its dot products,
-  // so a wave whose loads queue longer in the CU's memory pipeline delays
-  // no other wave.
-
-  // ---- R row groups x T sub-block pairs of weights per lane, by buffer loads.
-  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.wb, a.wb_records);
-  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.ws, a.ws_records);
-  const uint32_t pair0 = slice * (16 * kGemvT) + b;
-  const uint32_t row_bytes = a.bpr * kBytesPerBlock;
-  const uint32_t row0 = (rg_begin + team) * 4 + j;
-  const uint32_t wofs0 = row0 * row_bytes + pair0 * 16;
-  const uint32_t sofs0 = (row0 * a.bpr + (pair0 >> 2)) * kScalesPerBlock;
-  const uint32_t wstep = a.teams * 4 * row_bytes;
-  const uint32_t sstep = a.teams * 4 * a.bpr * kScalesPerBlock;
-  uint16_t dbits[kGemvMaxR][kGemvT];
-  u32x4 q[kGemvMaxR][kGemvT];
-  bool present[kGemvMaxR][kGemvT];
-#pragma unroll
-  for (uint32_t r = 0; r < kGemvMaxR; ++r) {
-    const bool rok = r < a.rgs && rg_begin + team + r * a.teams < rg_end;
-#pragma unroll
-    for (uint32_t t = 0; t < kGemvT; ++t) {
-      present[r][t] = rok && pair0 + 16 * t < a.npairs;
-      const uint32_t so = present[r][t] ? sofs0 + r * sstep + t * 8 : kOutOfRange;
-      dbits[r][t] = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
-    }
-  }
-  // scales ahead of the codes: the first row group's wait must not cover the
-  // later groups' weights
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (uint32_t r = 0; r < kGemvMaxR; ++r)
-#pragma unroll
-    for (uint32_t t = 0; t < kGemvT; ++t) {
-      const uint32_t wo = present[r][t] ? wofs0 + r * wstep + t * 256 : kOutOfRange;
-      q[r][t] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 0);
-    }
-
-  const uint32_t cg = 8 * (lane & 15);  // this lane's copy in the codebook half
-  const uint32_t cs = kSignHalf + cg;   // and in the sign half
-
-  // Dot products and output of activation row `mrow`, whose digits are in
-  // LDS.  Called once for row 0 outside any loop: inside the row loop the
-  // activation reloads of later rows would make the compiler's load-count
-  // bookkeeping wait for every weight before the first row group.
-  auto compute_row = [&](uint32_t mrow) {
-    // ---- per-lane activation registers for this wave's slice.  Lane (b, j)
-    // holds digit plane j (j < 3; row 3 of A is zero) of both sub-blocks of
-    // pair  p = pair0 + 16 t.
-    uint32_t xr[kGemvT][2][8];
-    float xs[kGemvT][2];
-#pragma unroll
-    for (uint32_t t = 0; t < kGemvT; ++t) {
-      const uint32_t pair = pair0 + 16 * t;
-      const bool ok = pair < a.npairs;
+  // ---- dot products of one tile
+  const uint32_t cg = 16 * (lane & (TL::kGridCopies - 1));  // this lane's codebook copy
+  const uint32_t cs = TL::kSignBase + 8 * (lane & (TL::kSignCopies - 1));
+  uint32_t xr[2][8];  // digit plane j of the tile's two sub-blocks (j = 3: zero)
+  float xs[2];        // their chunk scales
+  uint32_t cur_slice;
+  u32x4 q[kTilesPerWave];
+  float acc[kTilesPerWave];
+  // This lane's partial of tile k (before the sum over the 16 blocks).
+  auto compute_tile = [&](uint32_t k) -> float {
+    const uint32_t tau = t0 + k;
+    const uint32_t slice = tau / n_rg;
+    const uint32_t rgl = tau - slice * n_rg;
+    const uint32_t pair = slice * kSlicePairs + b;
+    const bool pair_ok = pair < a.npairs;
+    if (slice != cur_slice) {  // uniform
+      cur_slice = slice;
 #pragma unroll
       for (uint32_t h = 0; h < 2; ++h) {
         const uint32_t sb = 2 * pair + h;
-        xs[t][h] = ok ? xsc[sb] : 0.0f;
-        if (ok && j < 3) {
+        xs[h] = pair_ok ? xsc[sb] : 0.0f;
+        if (pair_ok && j < 3) {
           const u32x4* src = reinterpret_cast<const u32x4*>(xdig + j * a.plane_stride + sb * 32);
           const u32x4 lo = src[0], hi = src[1];
-          xr[t][h][0] = lo.x; xr[t][h][1] = lo.y; xr[t][h][2] = lo.z; xr[t][h][3] = lo.w;
-          xr[t][h][4] = hi.x; xr[t][h][5] = hi.y; xr[t][h][6] = hi.z; xr[t][h][7] = hi.w;
+          xr[h][0] = lo.x; xr[h][1] = lo.y; xr[h][2] = lo.z; xr[h][3] = lo.w;
+          xr[h][4] = hi.x; xr[h][5] = hi.y; xr[h][6] = hi.z; xr[h][7] = hi.w;
         } else {
 #pragma unroll
-          for (int k = 0; k < 8; ++k) xr[t][h][k] = 0u;
+          for (int kk = 0; kk < 8; ++kk) xr[h][kk] = 0u;
         }
       }
     }
-
-    // ---- the dot products, one 4-row group at a time.
+    const uint32_t rl = rgl * 4 + j;
+    const bool ok = pair_ok && row_begin + rl < a.out_dim;
+    const float d = ok ? half_bits_to_float(sscale[rl * a.bpr + (pair >> 2)]) : 0.0f;
+    pin_here(q[k]);
+    const uint32_t words[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
+    v4i c[2];
 #pragma unroll
-    for (uint32_t r = 0; r < kGemvMaxR; ++r) {
-      const uint32_t rg = rg_begin + team + r * a.teams;
-      if (r >= a.rgs || rg >= rg_end) break;  // wave-uniform
-      float acc = 0.0f;
+    for (uint32_t h = 0; h < 2; ++h) {
+      const uint32_t aux_g = words[2 * h];
+      const uint32_t aux_s = words[2 * h + 1];
+      const uint32_t ga[4] = {perm_addr<0>(aux_g, cg), perm_addr<1>(aux_g, cg),
+                              perm_addr<2>(aux_g, cg), perm_addr<3>(aux_g, cg)};
+      const uint32_t sa[4] = {sign_addr<kWide, 0>(aux_s, cs), sign_addr<kWide, 1>(aux_s, cs),
+                              sign_addr<kWide, 2>(aux_s, cs), sign_addr<kWide, 3>(aux_s, cs)};
+      u32x4 gv[4];
+      u32x2 sm[4];
 #pragma unroll
-      for (uint32_t t = 0; t < kGemvT; ++t) {
-        pin_here(q[r][t], dbits[r][t]);
-        const float d = half_bits_to_float(dbits[r][t]);
-        const uint32_t words[4] = {q[r][t].x, q[r][t].y, q[r][t].z, q[r][t].w};
-        // signed int8 weights of both sub-blocks of the pair
-        uint32_t w[2][8];
-#pragma unroll
-        for (uint32_t h = 0; h < 2; ++h) {
-          const uint32_t aux_g = words[2 * h];
-          const uint32_t aux_s = words[2 * h + 1];
-          // sign index g sits in byte g of aux_s << g, under one unrelated bit
-          const uint32_t sa[4] = {aux_s, aux_s << 1, aux_s << 2, aux_s << 3};
-          const uint32_t ga[4] = {table_addr<0>(aux_g, cg), table_addr<1>(aux_g, cg),
-                                  table_addr<2>(aux_g, cg), table_addr<3>(aux_g, cg)};
-          const uint32_t ma[4] = {table_addr<0>(sa[0], cs), table_addr<1>(sa[1], cs),
-                                  table_addr<2>(sa[2], cs), table_addr<3>(sa[3], cs)};
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const u32x2 gv = lds_load_u2(ga[g]);
-            const u32x2 sm = lds_load_u2(ma[g]);
-            w[h][2 * g] = apply_signs(gv.x, sm.x);
-            w[h][2 * g + 1] = apply_signs(gv.y, sm.y);
-          }
-        }
-        // two independent accumulation chains, interleaved
-        v4i c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          c0 = mfma4x4((int)xr[t][0][k], (int)w[0][k], c0);
-          c1 = mfma4x4((int)xr[t][1][k], (int)w[1][k], c1);
-        }
-        // c[p] = sum over the 32 columns of digit-plane p times w
-        const float f0 = fmaf((float)(c0[2] * 256 + c0[1]), 256.0f, (float)c0[0]);
-        const float f1 = fmaf((float)(c1[2] * 256 + c1[1]), 256.0f, (float)c1[0]);
-        const float coef0 = (float)((words[1] >> 27) | 1u) * (d * xs[t][0]);
-        const float coef1 = (float)((words[3] >> 27) | 1u) * (d * xs[t][1]);
-        acc = fmaf(f0, coef0, acc);
-        acc = fmaf(f1, coef1, acc);
+      for (int g = 0; g < 4; ++g) {
+        gv[g] = lds_u4(ga[g]);
+        sm[g] = lds_u2(sa[g]);
       }
-      acc = sum_over_blocks(acc);
-      if (lane < 4) red[((rg - rg_begin) * a.slices + slice) * 4 + j] = acc;
-      // keep row groups apart: interleaving them only raises register pressure
-      __builtin_amdgcn_sched_barrier(0);
+      // signed int8 weights of sub-block h: g where the mask is clear, -g where set
+      uint32_t w[8];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        w[2 * g] = bit_select(sm[g].x, gv[g].z, gv[g].x);
+        w[2 * g + 1] = bit_select(sm[g].y, gv[g].w, gv[g].y);
+      }
+      c[h] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) c[h] = mfma4x4((int)xr[h][kk], (int)w[kk], c[h]);
     }
-    __syncthreads();
-    // ---- the K-slices of each row, added in slice order.
-    const uint32_t rows_here = (rg_end > rg_begin) ? (rg_end - rg_begin) * 4 : 0;
-    for (uint32_t rr = tid; rr < rows_here; rr += nthreads) {
-      const uint32_t row = rg_begin * 4 + rr;
-      const float* p = red + (rr >> 2) * a.slices * 4 + (rr & 3);
+    // c[h][p] = sum over the 32 columns of digit plane p times w
+    const float f0 = fmaf((float)(c[0][2] * 256 + c[0][1]), 256.0f, (float)c[0][0]);
+    const float f1 = fmaf((float)(c[1][2] * 256 + c[1][1]), 256.0f, (float)c[1][0]);
+    const float coef0 = (float)((words[1] >> 27) | 1u) * (d * xs[0]);
+    const float coef1 = (float)((words[3] >> 27) | 1u) * (d * xs[1]);
+    return fmaf(f1, coef1, f0 * coef0);
+  };
+  // Row sums of the chunk's tiles for activation row mrow, into out.
+  auto reduce_and_store = [&](uint32_t mrow) {
+#pragma unroll
+    for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+      if (k >= cnt) break;  // uniform
+      const uint32_t tau = t0 + k;
+      const uint32_t slice = tau / n_rg;
+      const uint32_t rgl = tau - slice * n_rg;
+      const float v = sum_over_blocks(acc[k]);
+      if (lane < 4) red[(rgl * a.nslices + slice) * 4 + j] = v;
+    }
+    sync();
+    for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
+      const float* p = red + (rl >> 2) * a.nslices * 4 + (rl & 3);
       float sum = 0.0f;
-      for (uint32_t sl = 0; sl < a.slices; ++sl) sum += p[sl * 4];
-      if (row < a.out_dim) a.out[(size_t)mrow * a.out_dim + row] = sum;
+      for (uint32_t sl = 0; sl < a.nslices; ++sl) sum += p[sl * 4];
+      a.out[(size_t)mrow * a.out_dim + row_begin + rl] = sum;
     }
-    __syncthreads();  // xdig / red are rewritten for the next activation row
   };
 
-  compute_row(0);
-  for (uint32_t mrow = 1; mrow < a.m; ++mrow) {
-    load_x_tasks(0, (size_t)mrow * a.in_dim);
-    digitize_row(mrow);
-    digits_ready();
-    compute_row(mrow);
+  // ======== first chunk, activation row 0 (straight-line) ========
+  set_chunk(chunk);
+  // 1. set-up loads, ahead of every weight load
+  const uint32_t code = tid < 256 ? kGridCodesDev[tid] : 0u;
+  load_scales();
+  load_x(0, 0);
+  sync();
+  // 2. the first tiles
+#pragma unroll
+  for (uint32_t k = 0; k < kTilesAhead; ++k) q[k] = load_tile(k);
+  __builtin_amdgcn_sched_barrier(0);
+  // 3. tables (waves 0-7), digits (waves from 15 down), scales
+  if (tid < 256) {
+    store_grid_row<kWide>(lds, tid, grid_entry_from_code(code));
+    if (!kWide) store_sign_row<kWide>(lds, tid, expand_sign_mask((int)(tid & 127)), 0,
+                                      TL::kSignCopies);
+  } else if (kWide && tid < 512) {
+    const uint32_t i = (tid - 256) >> 1, half = tid & 1;
+    store_sign_row<kWide>(lds, i, expand_sign_mask((int)i), half * 16, 16);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  digitize_row(0);
+  stage_scales();
+  sync();
+  // 4. issue tile k + 2, compute tile k
+  cur_slice = ~0u;
+#pragma unroll
+  for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+    if (k + kTilesAhead < kTilesPerWave) q[k + kTilesAhead] = load_tile(k + kTilesAhead);
+    __builtin_amdgcn_sched_barrier(0);
+    acc[k] = 0.0f;
+    if (k < cnt) acc[k] = compute_tile(k);  // uniform
+  }
+  reduce_and_store(0);
+
+  // ======== further activation rows and chunks ========
+  if constexpr (!kMulti) return;
+  for (;;) {
+    for (uint32_t mrow = 1; mrow < a.m; ++mrow) {
+      sync();  // digits and partial sums are rewritten
+      load_x(0, mrow);
+      digitize_row(mrow);
+      sync();
+      cur_slice = ~0u;
+#pragma unroll
+      for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+        acc[k] = 0.0f;
+        if (k < cnt) acc[k] = compute_tile(k);
+      }
+      reduce_and_store(mrow);
+    }
+    chunk += gridDim.x;
+    if (chunk >= a.nchunks) break;
+    set_chunk(chunk);
+    load_scales();
+#pragma unroll
+    for (uint32_t k = 0; k < kTilesPerWave; ++k) q[k] = load_tile(k);
+    sync();  // scales and partial sums of the previous chunk consumed
+    stage_scales();
+    if (a.m > 1) {
+      load_x(0, 0);
+      digitize_row(0);
+    }
+    sync();
+    cur_slice = ~0u;
+#pragma unroll
+    for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+      acc[k] = 0.0f;
+      if (k < cnt) acc[k] = compute_tile(k);
+    }
+    reduce_and_store(0);
   }
 }
 
@@ -423,78 +565,112 @@ __global__ __launch_bounds__(kGemvMaxWaves * 64) void iq2xxs_gemv_kernel(GemvArg
 // Launch policy.
 // ---------------------------------------------------------------------------
 struct GemvPlan {
-  uint32_t slices, teams, rgs, rg_per_wg, xt, grid, threads, plane_stride;
+  uint32_t nslices, rg_per_chunk, nchunks, grid, ntasks, xt, plane_stride;
+  uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs;
   size_t lds;
+  bool wide;
 };
 
-// Shape of the launch for out_dim x in_dim on num_cus CUs.  One workgroup per
-// CU when the row groups allow: its waves are split into `slices` K-ranges of
-// 32 sub-block pairs and `teams` row sets; each wave holds at most kGemvMaxR
-// row groups of weights in registers.  False when the shape does not fit.
-static bool plan_gemv(uint32_t out_dim, uint32_t in_dim, int num_cus, GemvPlan* p) {
+static uint32_t align16(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
+
+// Launch shape for m x out_dim x in_dim on num_cus CUs; false when the shape
+// does not fit (LDS budget, 31-bit buffer offsets).
+static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, int num_cus,
+                      GemvPlan* p) {
   const uint64_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t npairs = bpr * 4;
   const uint64_t nsb = bpr * 8;
+  const uint64_t esize = x_dtype == 0 ? 4 : 2;
   if ((uint64_t)out_dim * bpr * kBytesPerBlock > kOutOfRange - 4096) return false;
-  const uint32_t slices = (uint32_t)((npairs + 16 * kGemvT - 1) / (16 * kGemvT));
-  if (slices > kGemvMaxWaves) return false;
-  const uint32_t teams_max = kGemvMaxWaves / slices;
-  const uint32_t n_rg = (out_dim + 3) / 4;
-  const uint32_t cus = num_cus > 0 ? (uint32_t)num_cus : 1;
-  const uint32_t target = (n_rg + cus - 1) / cus;  // row groups per workgroup
-  uint32_t rgs = (target + teams_max - 1) / teams_max;
-  if (rgs < 1) rgs = 1;
-  if (rgs > kGemvMaxR) rgs = kGemvMaxR;
-  uint32_t teams = (target + rgs - 1) / rgs;
-  if (teams > teams_max) teams = teams_max;
-  if (teams < 1) teams = 1;
-  p->slices = slices;
-  p->teams = teams;
-  p->rgs = rgs;
-  p->rg_per_wg = teams * rgs;
-  p->grid = (n_rg + p->rg_per_wg - 1) / p->rg_per_wg;
-  p->threads = 64 * slices * teams;
-  const uint64_t ntasks = nsb * 4;
-  p->xt = (uint32_t)((ntasks + p->threads - 1) / p->threads);  // capped per variant at launch
+  if ((uint64_t)m * in_dim * esize > kOutOfRange - 4096) return false;
+  const uint64_t nslices = (npairs + kSlicePairs - 1) / kSlicePairs;
+  const uint64_t n_rg = (out_dim + 3) / 4;
+  const uint64_t cus = num_cus > 0 ? (uint64_t)num_cus : 1;
+  const uint64_t target = (n_rg + cus - 1) / cus;  // row groups per CU
+  uint64_t rg_per_chunk = (kGemvWaves * kTilesPerWave) / nslices;
+  if (rg_per_chunk < 1) return false;
+  // as few chunks per workgroup as the tile budget allows, evenly sized
+  const uint64_t per_wg_chunks = (target + rg_per_chunk - 1) / rg_per_chunk;
+  rg_per_chunk = (target + per_wg_chunks - 1) / per_wg_chunks;
+  if (rg_per_chunk * 4 * bpr > (uint64_t)kScaleLoads * kGemvThreads) {
+    rg_per_chunk = (kScaleLoads * kGemvThreads) / (4 * bpr);
+    if (rg_per_chunk < 1) return false;
+  }
+  p->nslices = (uint32_t)nslices;
+  p->rg_per_chunk = (uint32_t)rg_per_chunk;
+  p->nchunks = (uint32_t)((n_rg + rg_per_chunk - 1) / rg_per_chunk);
+  p->grid = p->nchunks < cus ? p->nchunks : (uint32_t)cus;
+  p->ntasks = (uint32_t)(nsb * 4);
+  // two rounds' worth of activations per thread at most (more would spill);
+  // longer rows digitise in further rounds
+  p->xt = p->ntasks <= kGemvThreads ? 1 : 2;
   p->plane_stride = (uint32_t)(nsb * 32 + 16);
-  p->lds = kTableBytes + nsb * 4 + 3 * (uint64_t)p->plane_stride +
-           (uint64_t)p->rg_per_wg * slices * 16 + kGemvMaxWaves * 4;
+  const uint64_t scale_bytes = align16(rg_per_chunk * 4 * bpr * 2);
+  const uint64_t rest = scale_bytes + align16(nsb * 4) + 3ull * p->plane_stride +
+                        align16(rg_per_chunk * nslices * 16) + kGemvWaves * 4;
+  p->wide = GemvTables<true>::kBytes + rest <= kGemvLdsLimit;
+  const uint32_t tb = p->wide ? GemvTables<true>::kBytes : GemvTables<false>::kBytes;
+  p->scale_ofs = tb;
+  p->xsc_ofs = p->scale_ofs + (uint32_t)scale_bytes;
+  p->xdig_ofs = p->xsc_ofs + align16(nsb * 4);
+  p->red_ofs = p->xdig_ofs + 3 * p->plane_stride;
+  p->wred_ofs = p->red_ofs + align16(rg_per_chunk * nslices * 16);
+  p->lds = p->wred_ofs + kGemvWaves * 4;
   return p->lds <= kGemvLdsLimit;
 }
 
-bool gemv_supported(uint32_t out_dim, uint32_t in_dim) {
+bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
   GemvPlan p;
-  return plan_gemv(out_dim, in_dim, 1, &p);
+  return plan_gemv(m, out_dim, in_dim, x_dtype, 1, &p);
 }
 
-template <int XD, bool V>
-static hipError_t launch_gemv_t(GemvArgs a, const GemvPlan& p, hipStream_t stream) {
-  if (a.xt > gemv_max_xt<V>()) a.xt = gemv_max_xt<V>();
+template <int XD, bool V, bool W, int XT, bool Q, bool M>
+static hipError_t launch_gemv_t(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
   // The tables alone exceed the default 64 KB of dynamic LDS: raise the
   // limit once per instantiation.
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&iq2xxs_gemv_kernel<XD, V>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)kGemvLdsLimit);
+    hipError_t e =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&iq2xxs_gemv_kernel<XD, V, W, XT, Q, M>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsLimit);
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
-  hipLaunchKernelGGL((iq2xxs_gemv_kernel<XD, V>), dim3(p.grid), dim3(p.threads), p.lds, stream, a);
+  hipLaunchKernelGGL((iq2xxs_gemv_kernel<XD, V, W, XT, Q, M>), dim3(p.grid), dim3(kGemvThreads),
+                     p.lds, stream, a);
   return hipGetLastError();
+}
+
+template <int XD, bool V, bool W, bool Q>
+static hipError_t launch_gemv_m(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
+  const bool multi = a.m > 1 || a.nchunks > p.grid;
+  if (multi)
+    return p.xt <= 1 ? launch_gemv_t<XD, V, W, 1, Q, true>(a, p, stream)
+                     : launch_gemv_t<XD, V, W, 2, Q, true>(a, p, stream);
+  return p.xt <= 1 ? launch_gemv_t<XD, V, W, 1, Q, false>(a, p, stream)
+                   : launch_gemv_t<XD, V, W, 2, Q, false>(a, p, stream);
+}
+
+template <int XD, bool V, bool W>
+static hipError_t launch_gemv_xt(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
+  return a.w8a8 ? launch_gemv_m<XD, V, W, true>(a, p, stream)
+                : launch_gemv_m<XD, V, W, false>(a, p, stream);
 }
 
 template <int XD>
 static hipError_t launch_gemv_v(const GemvArgs& a, const GemvPlan& p, bool vec,
                                 hipStream_t stream) {
-  return vec ? launch_gemv_t<XD, true>(a, p, stream) : launch_gemv_t<XD, false>(a, p, stream);
+  if (vec) return p.wide ? launch_gemv_xt<XD, true, true>(a, p, stream)
+                         : launch_gemv_xt<XD, true, false>(a, p, stream);
+  return p.wide ? launch_gemv_xt<XD, false, true>(a, p, stream)
+                : launch_gemv_xt<XD, false, false>(a, p, stream);
 }
 
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream) {
   GemvPlan p;
-  if (!plan_gemv(out_dim, in_dim, num_cus, &p)) return hipErrorInvalidValue;
+  if (!plan_gemv(m, out_dim, in_dim, x_dtype, num_cus, &p)) return hipErrorInvalidValue;
   GemvArgs a;
   a.x = x;
   a.wb = wb;
@@ -505,14 +681,19 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
   a.in_dim = in_dim;
   a.bpr = (in_dim + kQK - 1) / kQK;
   a.npairs = a.bpr * 4;
-  a.slices = p.slices;
-  a.teams = p.teams;
-  a.rgs = p.rgs;
-  a.rg_per_wg = p.rg_per_wg;
-  a.xt = p.xt;
+  a.nslices = p.nslices;
+  a.rg_per_chunk = p.rg_per_chunk;
+  a.nchunks = p.nchunks;
+  a.ntasks = p.ntasks;
   a.wb_records = out_dim * a.bpr * kBytesPerBlock;
   a.ws_records = out_dim * a.bpr * kScalesPerBlock;
+  a.x_records = m * in_dim * (x_dtype == 0 ? 4u : 2u);
   a.plane_stride = p.plane_stride;
+  a.scale_ofs = p.scale_ofs;
+  a.xsc_ofs = p.xsc_ofs;
+  a.xdig_ofs = p.xdig_ofs;
+  a.red_ofs = p.red_ofs;
+  a.wred_ofs = p.wred_ofs;
   a.w8a8 = w8a8 ? 1 : 0;
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&

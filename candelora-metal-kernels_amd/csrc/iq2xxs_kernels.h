@@ -16,9 +16,9 @@ hipError_t launch_iq2xxs_dequant(const uint8_t* wb, const uint8_t* ws, void* out
                                  hipStream_t stream);
 
 // Decode-shaped matmul (int8-MFMA GEMV), any m; shapes where gemv_supported()
-// holds (K up to about 31000, weights below 2 GB).  Needs 16-byte aligned
-// weight_bytes and 2-byte aligned weight_scales.
-bool gemv_supported(uint32_t out_dim, uint32_t in_dim);
+// holds (K up to about 31000, weights and x below 2 GB).  Needs 16-byte
+// aligned weight_bytes and 2-byte aligned weight_scales.
+bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype);
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream);
