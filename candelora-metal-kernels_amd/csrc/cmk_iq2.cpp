@@ -86,12 +86,17 @@ int current_cu_count(int* cus) {
 // Path decision shared by the launch, the workspace query and the path query.
 enum class Path { Gemv, Gemm, Simple };
 
-Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, bool wb_aligned16,
-                 bool ws_aligned2) {
+// Null pointers stand for allocator-aligned buffers (queries made before the
+// buffers exist).
+Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, const void* x,
+                 const void* wb, const void* ws) {
+  auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; };
   const bool half_x = x_dtype == CMK_F16 || x_dtype == CMK_BF16;
-  if (half_x && m > kGemvMaxM && ws_aligned2) return Path::Gemm;
+  if (half_x && m > kGemvMaxM && m <= UINT32_MAX &&
+      cmk::gemm_supported((uint32_t)m, out_dim, in_dim) && al(x, 16) && al(wb, 8) && al(ws, 2))
+    return Path::Gemm;
   if (m <= UINT32_MAX && cmk::gemv_supported((uint32_t)m, out_dim, in_dim, x_dtype) &&
-      wb_aligned16 && ws_aligned2)
+      al(wb, 16) && al(ws, 2))
     return Path::Gemv;
   return Path::Simple;
 }
@@ -180,7 +185,7 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
                            &dims);
   if (rc != CMK_OK) return rc;
   // Assume allocator-aligned buffers (hipMalloc gives 256-byte alignment).
-  Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, true, true);
+  Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, nullptr, nullptr, nullptr);
   // The simple path can still be chosen at launch for unaligned weights; report
   // the larger need so either choice is covered.
   size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, m);
@@ -193,8 +198,8 @@ int cmk_iq2_matmul_path(cmk_dtype x_dtype, size_t m, size_t out_dim, size_t in_d
                         cmk_act_quant_mode mode) {
   (void)mode;
   return choose_path((int)x_dtype, m, (uint32_t)(out_dim > UINT32_MAX ? UINT32_MAX : out_dim),
-                     (uint32_t)(in_dim > UINT32_MAX ? UINT32_MAX : in_dim), true,
-                     true) == Path::Gemm
+                     (uint32_t)(in_dim > UINT32_MAX ? UINT32_MAX : in_dim), nullptr, nullptr,
+                     nullptr) == Path::Gemm
              ? 1
              : 0;
 }
@@ -225,9 +230,7 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul out must be 4-byte aligned");
 
   const bool w8a8 = md == CMK_ACT_QUANT_W8A8;
-  Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, aligned(weight_bytes, 16),
-                       aligned(weight_scales, 2));
-  if (p == Path::Gemm && !aligned(weight_bytes, 8)) p = Path::Simple;
+  Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x, weight_bytes, weight_scales);
   const size_t need_ws = workspace_for(p, w8a8, m);
   if (need_ws > 0 && (workspace == nullptr || workspace_bytes < need_ws))
     return fail(CMK_ERR_INVALID_ARGUMENT,

@@ -1,9 +1,10 @@
 // iq2xxs_gemm.hip — prefill-shaped IQ2_XXS matmul (large m, x in f16/bf16).
 //
-// out[m, n] = sum_k x[m, k] * W[n, k] with W dequantised per tile into LDS in
-// the activation's type (f16 or bf16, each value the RNE of the exact fp32
-// weight, i.e. exactly what iq2_dequantize_to_f16 produces), then fed to
-// v_mfma_f32_16x16x32_{f16,bf16} with fp32 accumulation.
+// out[m, n] = sum_k x[m, k] * W[n, k], W dequantised per tile into LDS in the
+// activation's type, then fed to v_mfma_f32_16x16x32_{f16,bf16} with fp32
+// accumulation.  Every dequantised value is the single round-to-nearest-even
+// of the exact weight d*(2s+1)*g/8, i.e. exactly what iq2_dequantize_to_f16
+// produces.
 //
 // The reference has no dedicated prefill kernel: its iq2_xxs_matmul_kernel
 // (src/metal_src/iq2_matmul.metal:188-240) serves every m with one thread per
@@ -13,11 +14,25 @@
 // +-127) (exact small integers in f16/bf16) and the fp32 result is divided by
 // the row's inv, i.e. sum(q/inv * w) up to fp32 rounding.
 //
-// Tile: 128 (m) x 128 (n) x 64 (k) per workgroup of 4 waves (2 x 2), each wave
-// 64 x 64 = 4 x 4 MFMA tiles.  LDS rows are padded by 8 halves so the 16
-// rows read by one MFMA operand fall in different banks.
+// Work split.  A workgroup computes a 128 x BN tile of out (BN = 224 gives
+// 4 x 64 = 256 workgroups for m = 512, n = 14336: one per CU).  Its 8 waves
+// split into two roles around a double-buffered LDS stage of 32 columns of k
+// (one sub-block of every weight row):
+//  * waves 0-3 (consumers, 2 x 2): each owns a 64 x BN/2 block of the tile and
+//    runs the MFMAs of one stage while the next is being written;
+//  * waves 4-7 (producers): load the x tile and the weights' codes two stages
+//    ahead, and write a stage: x as is, W dequantised.
+// One barrier per stage separates writing a buffer from reading it.
+//
+// Dequantisation of a sub-block (32 weights of one row): the three level
+// values RNE(l*d*(2s+1)/8), l in {8, 25, 43}, are formed once in fp32 (exact
+// products) and packed into two dwords; a selector table (one v_perm selector
+// per pair of weights of each codebook entry) then assembles each pair with
+// one v_perm, and a sign table (16-bit sign masks) applies ksigns with one xor.
 //
 // Bound: MFMA (arithmetic intensity ~1200 flop/B at m = 512).
+#include <atomic>
+
 #include "iq2xxs_device.h"
 #include "iq2xxs_kernels.h"
 
@@ -26,41 +41,64 @@ namespace cmk {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
-constexpr int kBK = 64;
-constexpr int kLdsStride = kBK + 8;  // halves per LDS row
-constexpr int kGemmThreads = 256;
+constexpr int kGemmBM = 128;
+constexpr int kGemmBK = 32;                       // columns of k per stage
+constexpr int kGemmPitch = (kGemmBK + 8) * 2;     // LDS bytes per tile row (80)
+constexpr int kGemmThreads = 512;
+constexpr int kGemmProducer0 = 256;               // first producer thread
+constexpr int kGemmTableCopies = 16;              // lane l reads copy l & 15
+constexpr uint32_t kGemmSelBytes = 256 * kGemmTableCopies * 16;   // 64 KB
+constexpr uint32_t kGemmSignBytes = 128 * kGemmTableCopies * 16;  // 32 KB
+constexpr uint32_t kGemmLdsLimit = 160 * 1024;
+constexpr uint32_t kGemmOutOfRange = 0x80000000u;
+constexpr int kGemmBufferWord3 = 0x00020000;
 
-__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
-  return __half_as_ushort(__float2half_rn(v));
-}
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
-  uint32_t x = __float_as_uint(v);
-  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)(((x >> 16) & 0x8000u) | 0x7FC0u);
-  x += 0x7FFFu + ((x >> 16) & 1u);
-  return (uint16_t)(x >> 16);
-}
+template <int BN>
+struct GemmLayout {
+  static constexpr uint32_t kA = kGemmBM * kGemmPitch;  // bytes of the x tile
+  static constexpr uint32_t kB = BN * kGemmPitch;       // bytes of the weight tile
+  static constexpr uint32_t kStage = kA + kB;
+  static constexpr uint32_t kSel = 2 * kStage;          // selector table
+  static constexpr uint32_t kSign = kSel + kGemmSelBytes;
+  static constexpr uint32_t kTotal = kSign + kGemmSignBytes;
+  static constexpr int kNTiles = BN / 32;                // 16-wide MFMA tiles per consumer in n
+};
 
 template <bool kBf16>
-__device__ __forceinline__ uint16_t to_operand(float v) {
-  return kBf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+__device__ __forceinline__ float4v mfma16(const u32x4& a, const u32x4& b, float4v c) {
+  if constexpr (kBf16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
+                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
 }
 
+// Two floats as a packed pair of f16 / bf16 (each one round-to-nearest-even).
 template <bool kBf16>
-__device__ __forceinline__ float4v mfma16(const uint4& a, const uint4& b, float4v c) {
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   if constexpr (kBf16) {
-    bf16x8 av, bv;
-    __builtin_memcpy(&av, &a, 16);
-    __builtin_memcpy(&bv, &b, 16);
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, c, 0, 0, 0);
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
   } else {
-    half8 av, bv;
-    __builtin_memcpy(&av, &a, 16);
-    __builtin_memcpy(&bv, &b, 16);
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, c, 0, 0, 0);
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
   }
+}
+
+__device__ __forceinline__ u32x4 gemm_lds_u4(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
+      static_cast<uintptr_t>(addr));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                           kGemmBufferWord3);
 }
 
 struct GemmArgs {
@@ -69,161 +107,199 @@ struct GemmArgs {
   const uint8_t* ws;
   float* out;
   const float* row_inv;  // W8A8 per-row inv scale, or null
-  uint32_t m, out_dim, in_dim, bpr, nk;  // nk = ceil(in_dim / 64)
+  uint32_t m, out_dim, in_dim, bpr, nk;  // nk = ceil(in_dim / 32)
+  uint32_t x_records, wb_records, ws_records;
 };
 
-// Staged global data for one k-step.
-struct Stage {
-  uint4 xa[4];     // 4 x 8 halves of the x tile (rows tid/8 + 32*i, cols 8*(tid%8))
-  uint2 q;         // this thread's sub-block codes
-  uint32_t dbits;  // fp16 d of its block
-};
-
-template <bool kBf16, bool kVecX>
-__device__ __forceinline__ void load_stage(const GemmArgs& a, uint32_t m0, uint32_t n0, uint32_t kt,
-                                           int tid, Stage& s) {
-  const uint32_t c = kt * kBK + 8 * (tid & 7);
+// Builds the selector and sign tables (all copies) with the workgroup's 512
+// threads: 256 selector entries and 128 sign entries, 16 copies each.
+template <int BN>
+__device__ __forceinline__ void build_gemm_tables(uint8_t* lds, uint32_t tid) {
+  using L = GemmLayout<BN>;
+  for (uint32_t u = tid; u < 256 + 128; u += kGemmThreads) {
+    u32x4 v;
+    uint32_t base;
+    if (u < 256) {
+      // pair p of entry u: bytes (2c, 2c+1) of level code c of each weight
+      const uint32_t code = kGridCodesDev[u];
+      uint32_t w[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t r = m0 + (tid >> 3) + 32 * i;
-    if (kVecX) {
-      if (r < a.m && c < a.in_dim)
-        s.xa[i] = *reinterpret_cast<const uint4*>(a.x + (size_t)r * a.in_dim + c);
-      else
-        s.xa[i] = make_uint4(0, 0, 0, 0);
-    } else {
-      uint16_t e[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        e[k] = (r < a.m && c + k < a.in_dim) ? a.x[(size_t)r * a.in_dim + c + k] : (uint16_t)0;
-      s.xa[i] = make_uint4(e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
-                           e[6] | (e[7] << 16));
-    }
-  }
-  // W: 128 rows x 2 sub-blocks; thread -> (row tid/2, sub-block tid%2).
-  const uint32_t row = n0 + (tid >> 1);
-  const uint32_t sb = kt * 2 + (tid & 1);
-  if (row < a.out_dim) {
-    const size_t block = (size_t)row * a.bpr + sb / 8;
-    s.q = *reinterpret_cast<const uint2*>(a.wb + block * kBytesPerBlock + (sb % 8) * 8);
-    s.dbits = *reinterpret_cast<const uint16_t*>(a.ws + block * kScalesPerBlock);
-  } else {
-    s.q = make_uint2(0, 0);
-    s.dbits = 0;
-  }
-}
-
-template <bool kBf16>
-__device__ __forceinline__ void store_stage(const GemmArgs& a, const Stage& s, uint16_t* As,
-                                            uint16_t* Bs, const uint64_t* lds_grid,
-                                            const uint64_t* lds_smask, float inv0, float inv1,
-                                            float inv2, float inv3, int tid) {
-  // x tile -> LDS (optionally W8A8-quantised)
-  const float invs[4] = {inv0, inv1, inv2, inv3};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint4 v = s.xa[i];
-    if (a.row_inv) {
-      uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        float lo = kBf16 ? bf16_bits_to_float((uint16_t)w[k]) : half_bits_to_float((uint16_t)w[k]);
-        float hi = kBf16 ? bf16_bits_to_float((uint16_t)(w[k] >> 16))
-                         : half_bits_to_float((uint16_t)(w[k] >> 16));
-        float ql = fminf(fmaxf(roundf(lo * invs[i]), -127.0f), 127.0f);
-        float qh = fminf(fmaxf(roundf(hi * invs[i]), -127.0f), 127.0f);
-        w[k] = (uint32_t)to_operand<kBf16>(ql) | ((uint32_t)to_operand<kBf16>(qh) << 16);
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t c0 = (code >> (4 * p)) & 3u, c1 = (code >> (4 * p + 2)) & 3u;
+        w[p] = (2 * c0) | ((2 * c0 + 1) << 8) | ((2 * c1) << 16) | ((2 * c1 + 1) << 24);
       }
-      v = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-    *reinterpret_cast<uint4*>(As + ((tid >> 3) + 32 * i) * kLdsStride + 8 * (tid & 7)) = v;
-  }
-  // W sub-block -> 32 dequantised values
-  const float d = half_bits_to_float((uint16_t)s.dbits);
-  const float dl = (d * (0.5f + (float)(s.q.y >> 28))) * 0.25f;
-  uint16_t* dst = Bs + (tid >> 1) * kLdsStride + 32 * (tid & 1);
+      v = u32x4{w[0], w[1], w[2], w[3]};
+      base = L::kSel + u * kGemmTableCopies * 16;
+    } else {
+      const uint32_t i = u - 256;
+      const uint32_t s = i | ((__popc(i) & 1u) << 7);  // ksigns(i)
+      uint32_t w[4];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const uint64_t gv = lds_grid[(s.q.x >> (8 * g)) & 0xFFu];
-    const uint64_t sm = lds_smask[(s.q.y >> (7 * g)) & 0x7Fu];
-    uint32_t p[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float v0 = dl * (float)((gv >> (16 * k)) & 0xFFu);
-      float v1 = dl * (float)((gv >> (16 * k + 8)) & 0xFFu);
-      if ((sm >> (16 * k)) & 1u) v0 = -v0;
-      if ((sm >> (16 * k + 8)) & 1u) v1 = -v1;
-      p[k] = (uint32_t)to_operand<kBf16>(v0) | ((uint32_t)to_operand<kBf16>(v1) << 16);
+      for (int p = 0; p < 4; ++p)
+        w[p] = (((s >> (2 * p)) & 1u) ? 0x8000u : 0u) | (((s >> (2 * p + 1)) & 1u) ? 0x80000000u : 0u);
+      v = u32x4{w[0], w[1], w[2], w[3]};
+      base = L::kSign + i * kGemmTableCopies * 16;
     }
-    *reinterpret_cast<uint4*>(dst + 8 * g) = make_uint4(p[0], p[1], p[2], p[3]);
+#pragma unroll 4
+    for (uint32_t k = 0; k < (uint32_t)kGemmTableCopies; ++k)
+      *reinterpret_cast<u32x4*>(lds + base + 16 * ((k + u) & (kGemmTableCopies - 1))) = v;
   }
 }
 
-template <bool kBf16, bool kVecX>
+template <bool kBf16, int BN>
 __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
-  __shared__ __align__(16) uint16_t As[2][kBM * kLdsStride];
-  __shared__ __align__(16) uint16_t Bs[2][kBN * kLdsStride];
-  __shared__ uint64_t lds_grid[256];
-  __shared__ uint64_t lds_smask[128];
+  using L = GemmLayout<BN>;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t m0 = blockIdx.y * kGemmBM;
+  const uint32_t n0 = blockIdx.x * BN;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const uint32_t m0 = blockIdx.y * kBM;
-  const uint32_t n0 = blockIdx.x * kBN;
+  build_gemm_tables<BN>(lds, tid);
 
-  build_lds_tables(lds_grid, lds_smask, tid, kGemmThreads);
-
-  float inv[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-  if (a.row_inv) {
+  if (wave >= 4) {
+    // ======== producers ========
+    const uint32_t p = tid - kGemmProducer0;  // 0..255
+    const __amdgpu_buffer_rsrc_t rx = gemm_rsrc(a.x, a.x_records);
+    const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(a.wb, a.wb_records);
+    const __amdgpu_buffer_rsrc_t rs = gemm_rsrc(a.ws, a.ws_records);
+    // x tile: 128 rows x 32 halves = 512 chunks of 16 B, two per producer
+    // (row = c / 4, 16-byte column chunk c % 4).
+    uint32_t xrow[2], xinv_ok[2];
+    float xinv[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t r = m0 + (tid >> 3) + 32 * i;
-      inv[i] = r < a.m ? a.row_inv[r] : 1.0f;
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t c = p + 256 * u;
+      xrow[u] = m0 + (c >> 2);
+      xinv_ok[u] = xrow[u] < a.m;
+      xinv[u] = (a.row_inv && xinv_ok[u]) ? a.row_inv[xrow[u]] : 1.0f;
     }
+    // weight row of this producer (BN <= 256 rows: one sub-block each per stage)
+    const uint32_t wrow = n0 + p;
+    const bool wrow_ok = p < (uint32_t)BN && wrow < a.out_dim;
+    const uint32_t cs = 16 * (lane & (kGemmTableCopies - 1));
+
+    struct Regs {
+      u32x4 xv[2];
+      u32x2 q;
+      uint32_t dbits;
+    };
+    auto issue = [&](uint32_t kt, Regs& r) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t c = p + 256 * u;
+        const uint32_t col = kt * kGemmBK + 8 * (c & 3);
+        // in_dim % 8 == 0 and x 16-byte aligned on this path: a chunk is in or out
+        const bool ok = xinv_ok[u] && col < a.in_dim;
+        r.xv[u] = __builtin_amdgcn_raw_buffer_load_b128(
+            rx, ok ? ((xrow[u] * a.in_dim) + col) * 2 : kGemmOutOfRange, 0, 0);
+      }
+      const uint32_t sb = kt;  // sub-block index along the row
+      const uint32_t blk = sb >> 3;
+      const bool ok = wrow_ok && kt < a.nk;
+      r.q = __builtin_amdgcn_raw_buffer_load_b64(
+          rw, ok ? (wrow * a.bpr + blk) * kBytesPerBlock + (sb & 7) * 8 : kGemmOutOfRange, 0, 0);
+      r.dbits = __builtin_amdgcn_raw_buffer_load_b16(
+          rs, ok ? (wrow * a.bpr + blk) * kScalesPerBlock : kGemmOutOfRange, 0, 0);
+    };
+    auto write_stage = [&](uint32_t stage, const Regs& r) {
+      uint8_t* A = lds + stage * L::kStage;
+      uint8_t* B = A + L::kA;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint32_t c = p + 256 * u;
+        u32x4 v = r.xv[u];
+        if (a.row_inv) {
+          uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float lo = kBf16 ? bf16_bits_to_float((uint16_t)w[k]) : half_bits_to_float((uint16_t)w[k]);
+            const float hi = kBf16 ? bf16_bits_to_float((uint16_t)(w[k] >> 16))
+                                   : half_bits_to_float((uint16_t)(w[k] >> 16));
+            const float ql = fminf(fmaxf(roundf(lo * xinv[u]), -127.0f), 127.0f);
+            const float qh = fminf(fmaxf(roundf(hi * xinv[u]), -127.0f), 127.0f);
+            w[k] = pack2<kBf16>(ql, qh);
+          }
+          v = u32x4{w[0], w[1], w[2], w[3]};
+        }
+        *reinterpret_cast<u32x4*>(A + (c >> 2) * kGemmPitch + 16 * (c & 3)) = v;
+      }
+      if (p < (uint32_t)BN) {
+        const uint32_t aux_g = r.q.x, aux_s = r.q.y;
+        // exact fp32 level values l * d * (2s + 1) / 8, then one rounding each
+        const float tdf = half_bits_to_float((uint16_t)r.dbits) * (float)((aux_s >> 27) | 1u) * 0.125f;
+        const uint32_t pool_lo = pack2<kBf16>(8.0f * tdf, 25.0f * tdf);
+        const uint32_t pool_hi = pack2<kBf16>(43.0f * tdf, 0.0f);
+        uint8_t* dst = B + p * kGemmPitch;
+        // all table reads first: the stores below may alias them as far as the
+        // compiler knows, so interleaving would serialise on LDS latency
+        u32x4 sel[4], sgn[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t e = (aux_g >> (8 * g)) & 0xFFu;
+          const uint32_t i = (aux_s >> (7 * g)) & 0x7Fu;
+          sel[g] = gemm_lds_u4(L::kSel + e * (kGemmTableCopies * 16) + cs);
+          sgn[g] = gemm_lds_u4(L::kSign + i * (kGemmTableCopies * 16) + cs);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const u32x4 v = {__builtin_amdgcn_perm(pool_hi, pool_lo, sel[g].x) ^ sgn[g].x,
+                           __builtin_amdgcn_perm(pool_hi, pool_lo, sel[g].y) ^ sgn[g].y,
+                           __builtin_amdgcn_perm(pool_hi, pool_lo, sel[g].z) ^ sgn[g].z,
+                           __builtin_amdgcn_perm(pool_hi, pool_lo, sel[g].w) ^ sgn[g].w};
+          *reinterpret_cast<u32x4*>(dst + 16 * g) = v;
+        }
+      }
+    };
+
+    Regs r0, r1;
+    issue(0, r0);
+    issue(1, r1);
+    __syncthreads();  // tables ready
+    write_stage(0, r0);
+    __syncthreads();  // stage 0 ready
+    // iteration kt: consumers read stage kt & 1; producers write stage (kt+1) & 1
+    // from the registers loaded two iterations earlier, then reload them.
+    for (uint32_t kt = 0; kt < a.nk; kt += 2) {
+      issue(kt + 2, r0);
+      if (kt + 1 < a.nk) write_stage(1, r1);
+      __syncthreads();
+      if (kt + 1 >= a.nk) break;
+      issue(kt + 3, r1);
+      if (kt + 2 < a.nk) write_stage(0, r0);
+      __syncthreads();
+    }
+    return;
   }
 
-  float4v acc[4][4];
+  // ======== consumers ========
+  const uint32_t wm = wave >> 1, wn = wave & 1;
+  constexpr int NT = L::kNTiles;  // n tiles of 16 per consumer
+  float4v acc[4][NT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int jn = 0; jn < 4; ++jn) acc[i][jn] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int jn = 0; jn < NT; ++jn) acc[i][jn] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-  Stage st;
-  load_stage<kBf16, kVecX>(a, m0, n0, 0, tid, st);
+  const uint32_t lr = lane & 15;        // operand row within a 16-row tile
+  const uint32_t lk = 16 * (lane >> 4);  // byte offset of the lane's 8 k-values
   __syncthreads();  // tables ready
-  store_stage<kBf16>(a, st, As[0], Bs[0], lds_grid, lds_smask, inv[0], inv[1], inv[2], inv[3],
-                     tid);
-  __syncthreads();
-
-  const int lr = lane & 15;       // operand row within a 16-row tile
-  const int lk = 8 * (lane >> 4);  // operand k offset within a 32-wide k-step
+  __syncthreads();  // stage 0 ready
   for (uint32_t kt = 0; kt < a.nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < a.nk;
-    if (more) load_stage<kBf16, kVecX>(a, m0, n0, kt + 1, tid, st);
-    const uint16_t* A = As[cur];
-    const uint16_t* B = Bs[cur];
+    const uint8_t* A = lds + (kt & 1) * L::kStage;
+    const uint8_t* B = A + L::kA;
+    u32x4 af[4], bfr[NT];
 #pragma unroll
-    for (int ks = 0; ks < kBK / 32; ++ks) {
-      uint4 af[4], bfr[4];
+    for (int i = 0; i < 4; ++i)
+      af[i] = *reinterpret_cast<const u32x4*>(A + (wm * 64 + i * 16 + lr) * kGemmPitch + lk);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const uint4*>(A + (wm * 64 + i * 16 + lr) * kLdsStride +
-                                                ks * 32 + lk);
+    for (int jn = 0; jn < NT; ++jn)
+      bfr[jn] = *reinterpret_cast<const u32x4*>(B + (wn * (BN / 2) + jn * 16 + lr) * kGemmPitch + lk);
 #pragma unroll
-      for (int jn = 0; jn < 4; ++jn)
-        bfr[jn] = *reinterpret_cast<const uint4*>(B + (wn * 64 + jn * 16 + lr) * kLdsStride +
-                                                  ks * 32 + lk);
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int jn = 0; jn < 4; ++jn) acc[i][jn] = mfma16<kBf16>(af[i], bfr[jn], acc[i][jn]);
-    }
-    if (more)
-      store_stage<kBf16>(a, st, As[cur ^ 1], Bs[cur ^ 1], lds_grid, lds_smask, inv[0], inv[1],
-                         inv[2], inv[3], tid);
+      for (int jn = 0; jn < NT; ++jn) acc[i][jn] = mfma16<kBf16>(af[i], bfr[jn], acc[i][jn]);
     __syncthreads();
   }
 
@@ -236,8 +312,8 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       if (row >= a.m) continue;
       const float scale = a.row_inv ? a.row_inv[row] : 1.0f;
 #pragma unroll
-      for (int jn = 0; jn < 4; ++jn) {
-        const uint32_t col = n0 + wn * 64 + jn * 16 + (lane & 15);
+      for (int jn = 0; jn < NT; ++jn) {
+        const uint32_t col = n0 + wn * (BN / 2) + jn * 16 + (lane & 15);
         if (col < a.out_dim) {
           float v = acc[i][jn][r];
           if (a.row_inv) v = v / scale;
@@ -246,6 +322,30 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       }
     }
   }
+}
+
+// The x tile is loaded in 16-byte chunks that are wholly in or out of range
+// (in_dim % 8 == 0), and every buffer offset stays below kGemmOutOfRange.
+bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim) {
+  return in_dim % 8 == 0 && (uint64_t)m * in_dim * 2 < kGemmOutOfRange - 4096 &&
+         (uint64_t)out_dim * ((in_dim + kQK - 1) / kQK) * kBytesPerBlock < kGemmOutOfRange - 4096;
+}
+
+template <bool kBf16, int BN>
+static hipError_t launch_gemm_t(const GemmArgs& a, hipStream_t stream) {
+  using L = GemmLayout<BN>;
+  static std::atomic<bool> attr_set{false};
+  if (!attr_set.load()) {
+    hipError_t e =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&iq2xxs_gemm_kernel<kBf16, BN>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLdsLimit);
+    if (e != hipSuccess) return e;
+    attr_set.store(true);
+  }
+  dim3 grid((a.out_dim + BN - 1) / BN, (a.m + kGemmBM - 1) / kGemmBM);
+  hipLaunchKernelGGL((iq2xxs_gemm_kernel<kBf16, BN>), grid, dim3(kGemmThreads), L::kTotal, stream,
+                     a);
+  return hipGetLastError();
 }
 
 hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
@@ -261,23 +361,17 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
   a.out_dim = out_dim;
   a.in_dim = in_dim;
   a.bpr = (in_dim + kQK - 1) / kQK;
-  a.nk = (in_dim + kBK - 1) / kBK;
-  const bool vec = (in_dim % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
-  dim3 grid((out_dim + kBN - 1) / kBN, (m + kBM - 1) / kBM);
+  a.nk = (in_dim + kGemmBK - 1) / kGemmBK;
+  a.x_records = m * in_dim * 2;
+  a.wb_records = out_dim * a.bpr * kBytesPerBlock;
+  a.ws_records = out_dim * a.bpr * kScalesPerBlock;
+  // tile width: 224 when it fills the CUs better than 128
+  const uint64_t mt = (m + kGemmBM - 1) / kGemmBM;
+  const uint64_t t224 = mt * ((out_dim + 223) / 224), t128 = mt * ((out_dim + 127) / 128);
+  const bool wide = t224 >= 200 || t224 * 224 <= t128 * 128;
   const bool bf = x_dtype == 2;
-  if (bf) {
-    if (vec)
-      hipLaunchKernelGGL((iq2xxs_gemm_kernel<true, true>), grid, dim3(kGemmThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((iq2xxs_gemm_kernel<true, false>), grid, dim3(kGemmThreads), 0, stream, a);
-  } else {
-    if (vec)
-      hipLaunchKernelGGL((iq2xxs_gemm_kernel<false, true>), grid, dim3(kGemmThreads), 0, stream, a);
-    else
-      hipLaunchKernelGGL((iq2xxs_gemm_kernel<false, false>), grid, dim3(kGemmThreads), 0, stream,
-                         a);
-  }
-  return hipGetLastError();
+  if (wide) return bf ? launch_gemm_t<true, 224>(a, stream) : launch_gemm_t<false, 224>(a, stream);
+  return bf ? launch_gemm_t<true, 128>(a, stream) : launch_gemm_t<false, 128>(a, stream);
 }
 
 }  // namespace cmk

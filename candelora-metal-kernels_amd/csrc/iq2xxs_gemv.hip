@@ -246,8 +246,9 @@ struct GemvArgs {
 
 // XD: activation dtype (0 f32, 1 f16, 2 bf16); kVecX: activations can be read
 // as aligned 16-byte vectors; kWide: table layout; kXT: digitisation tasks
-// per thread per round; kW8A8: fake-quantise x per row first; kMulti: m > 1 or
-// more than one chunk per workgroup (the loops are compiled out otherwise).
+// per thread per round; kW8A8: fake-quantise x per row first; kMulti: m > 1,
+// more than one chunk per workgroup or more than one digitisation round (the
+// loops are compiled out otherwise).
 template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti>
 __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -385,9 +386,11 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     float inv_scale = 1.0f;
     if constexpr (kW8A8) inv_scale = w8a8_inv_scale(mrow);
     digitize_round(0, inv_scale);
-    for (uint32_t r0 = round; r0 < a.ntasks; r0 += round) {
-      load_x(r0, mrow);
-      digitize_round(r0, inv_scale);
+    if constexpr (kMulti) {
+      for (uint32_t r0 = round; r0 < a.ntasks; r0 += round) {
+        load_x(r0, mrow);
+        digitize_round(r0, inv_scale);
+      }
     }
   };
   auto sync = [&]() {
@@ -404,11 +407,26 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   uint32_t cur_slice;
   u32x4 q[kTilesPerWave];
   float acc[kTilesPerWave];
+  float dsc[kTilesPerWave];  // super-block scale d of each tile's (row, pair)
+  // d of all of this wave's tiles, from the staged scales (one LDS round trip).
+  auto load_tile_scales = [&]() {
+    uint32_t slice = t0 / n_rg;
+    uint32_t rgl = t0 - slice * n_rg;
+#pragma unroll
+    for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+      const uint32_t pair = slice * kSlicePairs + b;
+      const uint32_t rl = rgl * 4 + j;
+      const bool ok = k < cnt && pair < a.npairs && row_begin + rl < a.out_dim;
+      dsc[k] = ok ? half_bits_to_float(sscale[rl * a.bpr + (pair >> 2)]) : 0.0f;
+      if (++rgl == n_rg) {
+        rgl = 0;
+        ++slice;
+      }
+    }
+  };
   // This lane's partial of tile k (before the sum over the 16 blocks).
   auto compute_tile = [&](uint32_t k) -> float {
-    const uint32_t tau = t0 + k;
-    const uint32_t slice = tau / n_rg;
-    const uint32_t rgl = tau - slice * n_rg;
+    const uint32_t slice = (t0 + k) / n_rg;
     const uint32_t pair = slice * kSlicePairs + b;
     const bool pair_ok = pair < a.npairs;
     if (slice != cur_slice) {  // uniform
@@ -428,12 +446,10 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         }
       }
     }
-    const uint32_t rl = rgl * 4 + j;
-    const bool ok = pair_ok && row_begin + rl < a.out_dim;
-    const float d = ok ? half_bits_to_float(sscale[rl * a.bpr + (pair >> 2)]) : 0.0f;
-    pin_here(q[k]);
+    if constexpr (kMulti) pin_here(q[k]);
     const uint32_t words[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
-    v4i c[2];
+    // signed int8 weights of both sub-blocks: g where the mask is clear, -g where set
+    uint32_t w[2][8];
 #pragma unroll
     for (uint32_t h = 0; h < 2; ++h) {
       const uint32_t aux_g = words[2 * h];
@@ -449,17 +465,20 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         gv[g] = lds_u4(ga[g]);
         sm[g] = lds_u2(sa[g]);
       }
-      // signed int8 weights of sub-block h: g where the mask is clear, -g where set
-      uint32_t w[8];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        w[2 * g] = bit_select(sm[g].x, gv[g].z, gv[g].x);
-        w[2 * g + 1] = bit_select(sm[g].y, gv[g].w, gv[g].y);
+        w[h][2 * g] = bit_select(sm[g].x, gv[g].z, gv[g].x);
+        w[h][2 * g + 1] = bit_select(sm[g].y, gv[g].w, gv[g].y);
       }
-      c[h] = v4i{0, 0, 0, 0};
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) c[h] = mfma4x4((int)xr[h][kk], (int)w[kk], c[h]);
     }
+    // two independent accumulation chains, interleaved
+    v4i c[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      c[0] = mfma4x4((int)xr[0][kk], (int)w[0][kk], c[0]);
+      c[1] = mfma4x4((int)xr[1][kk], (int)w[1][kk], c[1]);
+    }
+    const float d = dsc[k];
     // c[h][p] = sum over the 32 columns of digit plane p times w
     const float f0 = fmaf((float)(c[0][2] * 256 + c[0][1]), 256.0f, (float)c[0][0]);
     const float f1 = fmaf((float)(c[1][2] * 256 + c[1][1]), 256.0f, (float)c[1][0]);
@@ -512,6 +531,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   stage_scales();
   sync();
   // 4. issue tile k + 2, compute tile k
+  load_tile_scales();
   cur_slice = ~0u;
 #pragma unroll
   for (uint32_t k = 0; k < kTilesPerWave; ++k) {
@@ -551,6 +571,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       digitize_row(0);
     }
     sync();
+    load_tile_scales();
     cur_slice = ~0u;
 #pragma unroll
     for (uint32_t k = 0; k < kTilesPerWave; ++k) {
@@ -643,7 +664,7 @@ static hipError_t launch_gemv_t(const GemvArgs& a, const GemvPlan& p, hipStream_
 
 template <int XD, bool V, bool W, bool Q>
 static hipError_t launch_gemv_m(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
-  const bool multi = a.m > 1 || a.nchunks > p.grid;
+  const bool multi = a.m > 1 || a.nchunks > p.grid || a.ntasks > kGemvThreads * p.xt;
   if (multi)
     return p.xt <= 1 ? launch_gemv_t<XD, V, W, 1, Q, true>(a, p, stream)
                      : launch_gemv_t<XD, V, W, 2, Q, true>(a, p, stream);

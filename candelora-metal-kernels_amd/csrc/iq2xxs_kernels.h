@@ -35,7 +35,10 @@ hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, c
                                        hipStream_t stream);
 
 // Prefill matmul (MFMA GEMM, weights dequantised into LDS as f16/bf16);
-// x_dtype must be 1 (f16) or 2 (bf16).  Needs 8-byte aligned weight_bytes.
+// x_dtype must be 1 (f16) or 2 (bf16), on shapes where gemm_supported() holds
+// (in_dim % 8 == 0, x and weights below 2 GB).  Needs 16-byte aligned x,
+// 8-byte aligned weight_bytes and 2-byte aligned weight_scales.
+bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim);
 hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               const float* row_inv, hipStream_t stream);

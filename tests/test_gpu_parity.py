@@ -255,3 +255,46 @@ def test_gemm_w8a8(pkg, oracle, inputs, dev):
     y64 = xq @ w.T
     cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,out_dim,in_dim", [(300, 2000, 2048), (129, 230, 264)])
+def test_gemm_ragged_tiles(pkg, oracle, inputs, dev, dtype, m, out_dim, in_dim):
+    """Partial row and column tiles of both tile widths, K not a multiple of 256."""
+    test_gemm_vs_dequant_matmul(pkg, oracle, inputs, dev, dtype, m, out_dim, in_dim)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("out_dim,in_dim", [(14336, 4096), (4096, 14336)])
+def test_gemm_full_size_vs_device_dequant(pkg, inputs, dev, dtype, out_dim, in_dim):
+    """Prefill shapes at full size (m = 512): the GEMM against an fp64 product with
+    the device dequantisation (bit-exact with the oracle, tested above)."""
+    m = 512
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim, seed=5)
+    wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim, seed=6), dtype, dev)
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F16, m, out_dim, in_dim) == "gemm"
+    y = pkg.iq2_matmul(xt, wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs).double()
+    w = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                  out_dtype=dtype).double()
+    x64 = xt.double()
+    y64 = x64 @ w.T
+    sc = x64.abs() @ w.abs().T
+    cond, rel = errors(y.cpu().numpy(), y64.cpu().numpy(), sc.cpu().numpy())
+    assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+
+
+def test_gemm_w8a8_bf16_ragged(pkg, oracle, inputs, dev):
+    m, out_dim, in_dim = 200, 450, 768
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim) * 3, torch.bfloat16, dev)
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim,
+                                             in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                             cfg).cpu().numpy()
+    xq = oracle.rowwise_qdq_w8a8(x_as_f32(xt), m, in_dim).astype(np.float64)
+    wbits = oracle.dequantize_bf16_bits(wb, ws, out_dim, in_dim).astype(np.uint32) << 16
+    w = wbits.view(np.float32).astype(np.float64)
+    y64 = xq @ w.T
+    cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
+    assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
