@@ -93,7 +93,7 @@ Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, const
   auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; };
   const bool half_x = x_dtype == CMK_F16 || x_dtype == CMK_BF16;
   if (half_x && m > kGemvMaxM && m <= UINT32_MAX &&
-      cmk::gemm_supported((uint32_t)m, out_dim, in_dim) && al(x, 16) && al(wb, 8) && al(ws, 2))
+      cmk::gemm_supported((uint32_t)m, out_dim, in_dim) && al(x, 16) && al(wb, 16) && al(ws, 2))
     return Path::Gemm;
   if (m <= UINT32_MAX && cmk::gemv_supported((uint32_t)m, out_dim, in_dim, x_dtype) &&
       al(wb, 16) && al(ws, 2))
@@ -101,9 +101,15 @@ Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, const
   return Path::Simple;
 }
 
-size_t workspace_for(Path p, bool w8a8, size_t m) {
-  if (!w8a8 || p == Path::Gemv) return 0;
+// Row scales first (256-byte aligned), then for the GEMM the quantised rows.
+size_t row_scale_bytes(size_t m) {
   return ((m * sizeof(float) + kWorkspaceAlign - 1) / kWorkspaceAlign) * kWorkspaceAlign;
+}
+
+size_t workspace_for(Path p, bool w8a8, size_t m, uint32_t in_dim) {
+  if (!w8a8 || p == Path::Gemv) return 0;
+  if (p == Path::Gemm) return row_scale_bytes(m) + cmk::gemm_w8a8_scratch_bytes((uint32_t)m, in_dim);
+  return row_scale_bytes(m);
 }
 
 // Shared validation of cmk_iq2_matmul / cmk_iq2_matmul_workspace_size.
@@ -188,8 +194,8 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
   Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, nullptr, nullptr, nullptr);
   // The simple path can still be chosen at launch for unaligned weights; report
   // the larger need so either choice is covered.
-  size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, m);
-  size_t need_simple = workspace_for(Path::Simple, md == CMK_ACT_QUANT_W8A8, m);
+  size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, m, dims.in_dim);
+  size_t need_simple = workspace_for(Path::Simple, md == CMK_ACT_QUANT_W8A8, m, dims.in_dim);
   *bytes = need > need_simple ? need : need_simple;
   return ok();
 }
@@ -231,14 +237,15 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
 
   const bool w8a8 = md == CMK_ACT_QUANT_W8A8;
   Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x, weight_bytes, weight_scales);
-  const size_t need_ws = workspace_for(p, w8a8, m);
+  const size_t need_ws = workspace_for(p, w8a8, m, dims.in_dim);
   if (need_ws > 0 && (workspace == nullptr || workspace_bytes < need_ws))
     return fail(CMK_ERR_INVALID_ARGUMENT,
                 "iq2_matmul workspace too small: got %zu expected at least %zu (see "
                 "cmk_iq2_matmul_workspace_size)",
                 workspace ? workspace_bytes : (size_t)0, need_ws);
-  if (need_ws > 0 && !aligned(workspace, 4))
-    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul workspace must be 4-byte aligned");
+  const size_t ws_align = p == Path::Gemm ? 16 : 4;
+  if (need_ws > 0 && !aligned(workspace, ws_align))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul workspace must be %zu-byte aligned", ws_align);
 
   int cus = 0;
   rc = current_cu_count(&cus);
@@ -256,8 +263,9 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
                                   dims.out_dim, dims.in_dim, w8a8, cus, s);
       break;
     case Path::Gemm:
-      e = cmk::launch_iq2xxs_gemm(x, (int)x_dtype, dims.m, weight_bytes, weight_scales, out,
-                                  dims.out_dim, dims.in_dim, row_inv, s);
+      e = cmk::launch_iq2xxs_gemm(
+          x, (int)x_dtype, dims.m, weight_bytes, weight_scales, out, dims.out_dim, dims.in_dim,
+          row_inv, row_inv ? static_cast<uint8_t*>(workspace) + row_scale_bytes(m) : nullptr, s);
       break;
     case Path::Simple:
       e = cmk::launch_iq2xxs_matmul_simple(x, (int)x_dtype, dims.m, weight_bytes, weight_scales,

@@ -36,11 +36,14 @@ hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, c
 
 // Prefill matmul (MFMA GEMM, weights dequantised into LDS as f16/bf16);
 // x_dtype must be 1 (f16) or 2 (bf16), on shapes where gemm_supported() holds
-// (in_dim % 8 == 0, x and weights below 2 GB).  Needs 16-byte aligned x,
-// 8-byte aligned weight_bytes and 2-byte aligned weight_scales.
+// (in_dim % 8 == 0, x and weights below 2 GB).  Needs 16-byte aligned x and
+// weight_bytes and 2-byte aligned weight_scales.
+// W8A8 (row_inv non-null) first writes the quantised activations to xq, which
+// holds gemm_w8a8_scratch_bytes(m, in_dim) bytes, 16-byte aligned.
 bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim);
+size_t gemm_w8a8_scratch_bytes(uint32_t m, uint32_t in_dim);
 hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              const float* row_inv, hipStream_t stream);
+                              const float* row_inv, void* xq, hipStream_t stream);
 
 }  // namespace cmk

@@ -126,7 +126,9 @@ def test_dequantize_validation(cabi):
 
 def test_workspace_and_path_queries(cabi):
     assert cabi.workspace_size(cabi.CMK_F16, 512, 14336, 4096) == 0
-    assert cabi.workspace_size(cabi.CMK_F16, 512, 14336, 4096, mode=cabi.CMK_ACT_QUANT_W8A8) == 2048
+    # W8A8 on the GEMM path: row scales (256-byte aligned) + quantised activations
+    assert (cabi.workspace_size(cabi.CMK_F16, 512, 14336, 4096, mode=cabi.CMK_ACT_QUANT_W8A8)
+            == 2048 + 512 * 4096 * 2)
     assert cabi.workspace_size(cabi.CMK_F32, 1, 4096, 4096, mode=cabi.CMK_ACT_QUANT_OFF) == 0
     assert cabi.matmul_path(cabi.CMK_F16, 512, 14336, 4096) == "gemm"
     assert cabi.matmul_path(cabi.CMK_BF16, 17, 14336, 4096) == "gemm"
