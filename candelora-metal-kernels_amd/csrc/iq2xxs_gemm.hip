@@ -15,28 +15,35 @@
 // GEMM runs on q and divides each fp32 result by its row's inv, i.e.
 // sum(q/inv * w) up to fp32 rounding.
 //
-// Work split.  A workgroup computes a 128 x BN tile of out (BN = 224 gives
-// 4 x 64 = 256 workgroups for m = 512, n = 14336: one per CU).  k advances in
-// stages of 64 columns (two 32-weight sub-blocks of every weight row).
-//  * Waves 0-3 (consumers, 2 x 2) each own a 64 x BN/2 block of the tile.  They
-//    load their activation fragments straight from global memory (L2-resident
-//    x, one stage ahead) and read the weight fragments from LDS.
-//  * Waves 4-7 (producers) own one weight row per lane: they load the row's
-//    codes 128 bytes (eight stages) at a time, dequantise one stage per step
-//    into a double-buffered LDS tile, and a barrier publishes each stage.
-// Only the weight tile passes through LDS: LDS writes run at about 100 B/clk
-// and reads at about 270 B/clk per CU on gfx950, and an activation tile in LDS
-// as well would cost more LDS time per stage than the stage's MFMAs take.
+// Work split.  A workgroup computes a BM x BN tile of out; k advances in
+// stages of 32 columns (one 32-weight sub-block of every weight row).  For
+// m = 512, n = 14336 the tile is 256 x 112: 2 x 128 = 256 workgroups, one per
+// CU, and every weight sub-block is dequantised by two CUs only.
+//  * Waves 0-3 (consumers) each own a 64 x BN/WN block of the tile.  They read
+//    fragments from LDS, issue MFMAs, and copy the activations of the stage two
+//    ahead into LDS with global-to-LDS DMA (buffer_load ... lds), which costs
+//    them no VALU work: on gfx950 a wave's VALU work does not overlap its own
+//    MFMAs, while VALU work of another wave on the same SIMD does.
+//  * Waves 4-7 (producers) dequantise the weights: two lanes per weight row,
+//    two 8-weight groups each per stage, with the table reads of the next
+//    stage in flight while the current one is assembled.  A barrier per stage
+//    publishes it.
+// Layout and load shapes follow measurements on gfx950: vector loads run at
+// full rate only when each quad of lanes reads 64 contiguous bytes; LDS reads
+// run at about 270 B/clk per CU when conflict-free, writes at about 100 B/clk;
+// VALU work of a wave sharing a SIMD with an MFMA stream issues at about one
+// instruction per 6-8 clocks.
 //
 // LDS layout (64 KB aligned tables, so one v_perm forms a selector address):
 //   [0, 64K)      selector table: 256 codebook entries x 16 copies x 16 B
 //   [64K, 96K)    sign table: 128 sign indices x 16 copies x 16 B
-//   [96K, ...)    two weight tiles of BN rows x 128 B, 16-byte chunk c of row
-//                 r stored at chunk position c ^ (r & 7) (conflict-free reads
-//                 of the MFMA fragment pattern; measured on gfx950).
+//   [96K, ...)    three activation tiles (BM rows x 64 B), then two weight
+//                 tiles (BN rows x 64 B); 16-byte chunk c of row r is stored
+//                 at position c ^ ((r >> 1) & 3), which makes the MFMA
+//                 fragment reads conflict-free.
 //
 // Dequantisation of a sub-block (32 weights of one row): the three level
-// values RNE(l*d*(2s+1)/8), l in {8, 25, 43}, are formed once in fp32 (exact
+// values RNE(l*d*(2s+1)/8), l in {8, 25, 43}, are formed in fp32 (exact
 // products) and packed into two dwords; the selector table (one v_perm
 // selector per pair of weights of each codebook entry) then assembles each
 // pair with one v_perm, and the sign table (16-bit sign masks) applies ksigns
@@ -55,26 +62,31 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kGemmBM = 128;
-constexpr int kGemmBK = 64;                  // columns of k per stage
-constexpr int kGemmRowBytes = kGemmBK * 2;   // LDS bytes per weight-tile row
+constexpr int kGemmBK = 32;                  // columns of k per stage
 constexpr int kGemmThreads = 512;
 constexpr int kGemmProducer0 = 256;          // first producer thread
-constexpr int kGemmGroup = 8;                // stages per 128-byte code load
+constexpr int kGemmUnroll = 16;              // producer steps per loop trip
 constexpr uint32_t kGemmSel = 0;             // selector table
 constexpr uint32_t kGemmSign = 0x10000;      // sign table
-constexpr uint32_t kGemmTiles = 0x18000;     // weight tiles
+constexpr uint32_t kGemmTiles = 0x18000;     // activation and weight tiles
 constexpr uint32_t kGemmLdsLimit = 160 * 1024;
 constexpr uint32_t kGemmOutOfRange = 0x80000000u;
 constexpr int kGemmBufferWord3 = 0x00020000;
 
-template <int BN>
+// Tile geometry: BM x BN per workgroup, consumer waves WM x WN of 64 x TN.
+template <int BM, int BN>
 struct GemmLayout {
-  static constexpr uint32_t kStage = BN * kGemmRowBytes;
-  static constexpr uint32_t kTotal = kGemmTiles + 2 * kStage;
-  static constexpr int kNTiles = BN / 32;  // 16-wide MFMA tiles per consumer in n
+  static constexpr int WM = BM / 64, WN = 4 / WM, TN = BN / WN;
+  static constexpr int NT = TN / 16;                  // 16-wide MFMA tiles per consumer in n
+  static constexpr uint32_t kAStage = BM * 64;        // one activation tile
+  static constexpr uint32_t kBStage = BN * 64;        // one weight tile
+  static constexpr uint32_t kA = kGemmTiles;          // three activation tiles
+  static constexpr uint32_t kB = kA + 3 * kAStage;    // two weight tiles
+  static constexpr uint32_t kTotal = kB + 2 * kBStage;
+  static constexpr int kDma = BM / 64;                // DMA instructions per consumer per stage
+  static_assert(WM * WN == 4 && TN % 16 == 0, "four consumer waves of whole MFMA tiles");
+  static_assert(2 * BN <= 256, "two producer lanes per weight row");
   static_assert(kTotal <= kGemmLdsLimit, "LDS budget");
-  static_assert((BN / 2) % 16 == 0, "consumer column block of whole MFMA tiles");
 };
 
 template <bool kBf16>
@@ -122,10 +134,22 @@ struct GemmArgs {
   float* out;
   const float* row_inv;  // W8A8 per-row inv scale, or null
   uint32_t m, out_dim, in_dim, bpr;
-  uint32_t nk;      // ceil(in_dim / 64) stages
-  uint32_t nk_pad;  // nk rounded up to whole pairs of code loads (2 kGemmGroup stages)
+  uint32_t nk;      // ceil(in_dim / 32) stages
+  uint32_t nk_pad;  // 1 + (nk - 1) rounded up to whole producer loop trips
   uint32_t x_records, wb_records, ws_records;
 };
+
+// Barrier of the consumer waves inside the main loop: waits until at most
+// kVm of this wave's DMAs are in flight and its LDS reads are done, then
+// s_barrier, without a memory fence (a workgroup fence would also wait for
+// the DMA of the stage after next).  The producers' side of every barrier is
+// a full __syncthreads, so their LDS writes are complete before it.  The
+// memory clobber keeps the compiler from moving LDS accesses across it.
+template <int kVm>
+__device__ __forceinline__ void consumer_barrier() {
+  static_assert(kVm >= 0 && kVm < 16, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kVm) : "memory");
+}
 
 // Builds the selector and sign tables (16 copies each) with the workgroup's
 // 512 threads: 256 selector entries and 128 sign entries, one per thread.
@@ -158,209 +182,236 @@ __device__ __forceinline__ void build_gemm_tables(uint32_t tid) {
   for (uint32_t k = 0; k < 16; ++k) gemm_lds_store(base + 16 * ((k + tid) & 15), v);
 }
 
-template <bool kBf16, int BN, bool kQ>
+template <bool kBf16, int BM, int BN, bool kQ>
 __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
-  using L = GemmLayout<BN>;
+  using L = GemmLayout<BM, BN>;
   extern __shared__ __align__(16) uint8_t lds[];
   (void)lds;  // addressed through the layout constants above
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t m0 = blockIdx.y * kGemmBM;
+  const uint32_t m0 = blockIdx.y * BM;
   const uint32_t n0 = blockIdx.x * BN;
 
   build_gemm_tables(tid);
 
   if (wave >= 4) {
-    // ======== producers: weight row n0 + p ========
+    // ======== producers: lanes 2r, 2r + 1 own weight row n0 + r ========
     const uint32_t p = tid - kGemmProducer0;  // 0..255
-    const bool row_ok = p < (uint32_t)BN && n0 + p < a.out_dim;
+    const uint32_t r = p >> 1, h = p & 1;     // row, group pair (groups 2h, 2h + 1)
+    const bool active = r < (uint32_t)BN;
+    const bool row_ok = active && n0 + r < a.out_dim;
     const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(a.wb, a.wb_records);
     const __amdgpu_buffer_rsrc_t rs = gemm_rsrc(a.ws, a.ws_records);
-    const uint32_t row_blk = (n0 + p) * a.bpr;
+    const uint32_t row_blk = (n0 + r) * a.bpr;
     const uint32_t cs = 16 * (lane & 15);  // table copy of this lane
-    const uint32_t wdst = kGemmTiles + p * kGemmRowBytes;
-    const uint32_t swz = p & 7;
+    const uint32_t wdst0 = L::kB + r * 64 + 16 * ((2 * h + 0) ^ ((r >> 1) & 3));
+    const uint32_t wdst1 = L::kB + r * 64 + 16 * ((2 * h + 1) ^ ((r >> 1) & 3));
 
-    // Codes of eight stages (blocks 2g, 2g+1 of the row: 128 bytes) and their
-    // two scales.  Past the row's end the loads read zeros or the next row:
-    // such stages are padding that no consumer reads.
+    // Codes of one block (eight stages) and its scale.  Past the row's end
+    // the loads read zeros or the next row: such stages are padding that no
+    // consumer reads.
     struct Codes {
-      u32x4 q[kGemmGroup];
-      uint32_t d[2];
+      u32x4 q[4];  // sub-blocks 2j, 2j + 1 of the block
+      uint32_t d;
     };
-    // Scales first, in a fixed order with the codes: a stage then waits only
-    // for loads of its own set, never for the set issued after it.
+    // The scale first and the order pinned: a stage then waits only for
+    // loads of its own set.
     auto load_codes = [&](uint32_t g, Codes& c) {
-      const uint32_t blk = row_blk + 2 * g;
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        c.d[h] = __builtin_amdgcn_raw_buffer_load_b16(
-            rs, row_ok ? (blk + h) * kScalesPerBlock : kGemmOutOfRange, 0, 0);
+      const uint32_t blk = row_blk + g;
+      c.d = __builtin_amdgcn_raw_buffer_load_b16(
+          rs, row_ok ? blk * kScalesPerBlock : kGemmOutOfRange, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < kGemmGroup; ++j)
+      for (int j = 0; j < 4; ++j)
         c.q[j] = __builtin_amdgcn_raw_buffer_load_b128(
             rw, row_ok ? blk * kBytesPerBlock + 16 * j : kGemmOutOfRange, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     };
-    // Dequantise one stage (sub-blocks 2s, 2s+1 of the row) into a tile.
-    auto write_stage = [&](uint32_t tile, const u32x4& q, uint32_t dbits) {
-      if (p >= (uint32_t)BN) return;
-      const float d = half_bits_to_float((uint16_t)dbits);
-      const uint32_t aux[2][2] = {{q.x, q.y}, {q.z, q.w}};
-      u32x4 sel[2][4], sgn[2][4];
+    // Dequantisation of this lane's two groups of a sub-block, in two parts:
+    // the table reads, then the assembly into weight tile t (one stage apart).
+    struct Tables {
+      u32x4 sel[2], sgn[2];
+    };
+    auto read_tables = [&](uint32_t aux_g, uint32_t aux_s, Tables& T) {
+      if (!active) return;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          // selector entry aux_g.byte(g): address (e << 8) | cs in one v_perm
-          const uint32_t sa = kGemmSel + __builtin_amdgcn_perm(aux[h][0], cs, 0x0C0C0000u | ((4u + g) << 8));
-          const uint32_t ia = kGemmSign + (__builtin_amdgcn_ubfe(aux[h][1], 7 * g, 7) << 8) + cs;
-          sel[h][g] = gemm_lds_u4(sa);
-          sgn[h][g] = gemm_lds_u4(ia);
-        }
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        // exact fp32 level values l * d * (2s + 1) / 8, then one rounding each
-        const float tdf = d * (float)((aux[h][1] >> 27) | 1u) * 0.125f;
-        const uint32_t pool_lo = pack2<kBf16>(8.0f * tdf, 25.0f * tdf);
-        const uint32_t pool_hi = pack2<kBf16>(43.0f * tdf, 0.0f);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const u32x4 v = {__builtin_amdgcn_perm(pool_hi, pool_lo, sel[h][g].x) ^ sgn[h][g].x,
-                           __builtin_amdgcn_perm(pool_hi, pool_lo, sel[h][g].y) ^ sgn[h][g].y,
-                           __builtin_amdgcn_perm(pool_hi, pool_lo, sel[h][g].z) ^ sgn[h][g].z,
-                           __builtin_amdgcn_perm(pool_hi, pool_lo, sel[h][g].w) ^ sgn[h][g].w};
-          gemm_lds_store(tile + wdst + 16 * ((4 * h + g) ^ swz), v);
-        }
+      for (int gg = 0; gg < 2; ++gg) {
+        const uint32_t g = 2 * h + gg;
+        // selector entry aux_g.byte(g): address (e << 8) | cs in one v_perm
+        T.sel[gg] = gemm_lds_u4(kGemmSel + __builtin_amdgcn_perm(aux_g, cs, 0x0C0C0000u | ((4u + g) << 8)));
+        T.sgn[gg] = gemm_lds_u4(kGemmSign + (__builtin_amdgcn_ubfe(aux_s, 7 * g, 7) << 8) + cs);
       }
     };
+    auto write_w = [&](uint32_t t, uint32_t aux_s, uint32_t dbits, const Tables& T) {
+      if (!active) return;
+      // exact fp32 level values l * d * (2s + 1) / 8, then one rounding each
+      const float tdf = half_bits_to_float((uint16_t)dbits) * (float)((aux_s >> 27) | 1u) * 0.125f;
+      const uint32_t pool_lo = pack2<kBf16>(8.0f * tdf, 25.0f * tdf);
+      const uint32_t pool_hi = pack2<kBf16>(43.0f * tdf, 0.0f);
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        const u32x4 v = {__builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].x) ^ T.sgn[gg].x,
+                         __builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].y) ^ T.sgn[gg].y,
+                         __builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].z) ^ T.sgn[gg].z,
+                         __builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].w) ^ T.sgn[gg].w};
+        gemm_lds_store((gg ? wdst1 : wdst0) + t * L::kBStage, v);
+      }
+    };
+    // codes of the stage at sub-block sb of its block, from set c
+    auto aux_of = [](const Codes& c, int sb, uint32_t& aux_g, uint32_t& aux_s) {
+      const u32x4& q = c.q[sb >> 1];
+      aux_g = (sb & 1) ? q.z : q.x;
+      aux_s = (sb & 1) ? q.w : q.y;
+    };
 
-    // Two code sets alternate (no register copies: a copy of a set still
-    // being loaded would wait for it).  Stage s goes to tile s & 1; the
-    // barrier after it publishes it.  The loop runs whole pairs of code loads
-    // (nk_pad stages) so that its body is one straight-line sequence and the
-    // compiler's wait counts stay exact.
     Codes c0, c1;
+    Tables t0, t1;
     load_codes(0, c0);
     load_codes(1, c1);
     __syncthreads();  // tables ready
-    for (uint32_t g = 0; g * kGemmGroup < a.nk_pad; g += 2) {
+    // prologue: stage 0, and the table reads of stage 1
+    {
+      uint32_t g0, s0v, g1, s1v;
+      aux_of(c0, 0, g0, s0v);
+      read_tables(g0, s0v, t0);
+      aux_of(c0, 1, g1, s1v);
+      read_tables(g1, s1v, t1);
+      write_w(0, s0v, c0.d, t0);
+    }
+    __syncthreads();  // stage 0 published
+    // Step s reads the tables of stage s + 1, writes stage s (weight tile
+    // s & 1) from the tables read one step earlier, and after the last stage
+    // of a block reloads that code set with the block two ahead.  A trip
+    // covers kGemmUnroll steps from s0 = 1 (mod 16), so every set choice below
+    // is a compile-time constant and the body is one straight-line sequence
+    // (exact wait counts).
+    for (uint32_t s0 = 1; s0 < a.nk_pad; s0 += kGemmUnroll) {
 #pragma unroll
-      for (int j = 0; j < kGemmGroup; ++j) {
-        write_stage((j & 1) * L::kStage, c0.q[j], c0.d[j >> 2]);
+      for (int j = 0; j < kGemmUnroll; ++j) {
+        const uint32_t s = s0 + j;
+        const int cj = 1 + j;  // s modulo 16
+        Codes& cc = ((cj >> 3) & 1) ? c1 : c0;        // block of stage s
+        Codes& cn = (((cj + 1) >> 3) & 1) ? c1 : c0;  // block of stage s + 1
+        Tables& tc = (cj & 1) ? t1 : t0;
+        Tables& tn = (cj & 1) ? t0 : t1;
+        uint32_t gn, sn, gc, sc;
+        aux_of(cn, (cj + 1) & 7, gn, sn);
+        read_tables(gn, sn, tn);
+        aux_of(cc, cj & 7, gc, sc);
+        write_w((uint32_t)(cj & 1), sc, cc.d, tc);
+        if ((cj & 7) == 7) load_codes((s >> 3) + 2, cc);
         __syncthreads();
       }
-      load_codes(g + 2, c0);
-#pragma unroll
-      for (int j = 0; j < kGemmGroup; ++j) {
-        write_stage((j & 1) * L::kStage, c1.q[j], c1.d[j >> 2]);
-        __syncthreads();
-      }
-      load_codes(g + 3, c1);
     }
     return;
   }
 
   // ======== consumers ========
-  const uint32_t wm = wave >> 1, wn = wave & 1;
-  constexpr int NT = L::kNTiles;
+  constexpr int NT = L::NT;
+  const uint32_t wm = wave / L::WN, wn = wave % L::WN;
   float4v acc[4][NT];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int jn = 0; jn < NT; ++jn) acc[i][jn] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Activation fragments: rows m0 + 64 wm + 16 i + (lane & 15), the lane's 8
-  // columns at 8 (lane >> 4) + 32 kh of the stage.  in_dim % 8 == 0 on this
-  // path, so a 16-byte chunk is wholly in or out of the row.
-  const __amdgpu_buffer_rsrc_t rx = gemm_rsrc(a.x, a.x_records);
-  uint32_t arow[4];
-  bool arow_ok[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t row = m0 + wm * 64 + i * 16 + (lane & 15);
-    arow_ok[i] = row < a.m;
-    arow[i] = row * a.in_dim * 2 + 16 * (lane >> 4);
-  }
-  const uint32_t acol = 8 * (lane >> 4);
-  struct AFrags {
-    u32x4 f[2][4];  // [kh][i]
+  // Fragment addresses: row (16-aligned base) + (lane & 15), chunk lane >> 4,
+  // stored at position chunk ^ ((row >> 1) & 3) = chunk ^ ((lane >> 1) & 3).
+  const uint32_t fpos = 16 * ((lane >> 4) ^ ((lane >> 1) & 3));
+  const uint32_t aofs = L::kA + (wm * 64 + (lane & 15)) * 64 + fpos;
+  const uint32_t bofs = L::kB + (wn * L::TN + (lane & 15)) * 64 + fpos;
+  struct Frags {
+    u32x4 a[4], b[NT];
   };
-  auto load_a = [&](uint32_t st, AFrags& A) {
+  // fragments of stage s: activation tile abuf (s % 3), weight tile s & 1
+  auto read_frags = [&](uint32_t abuf, uint32_t s, Frags& F) {
+    const uint32_t abase = aofs + abuf * L::kAStage;
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh)
+    for (int i = 0; i < 4; ++i) F.a[i] = gemm_lds_u4(abase + i * 16 * 64);
+    const uint32_t bbase = bofs + (s & 1) * L::kBStage;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool ok = arow_ok[i] && st * kGemmBK + 32 * kh + acol < a.in_dim;
-        A.f[kh][i] = __builtin_amdgcn_raw_buffer_load_b128(
-            rx, ok ? arow[i] + st * (kGemmBK * 2) + 64 * kh : kGemmOutOfRange, 0, 0);
-      }
+    for (int jn = 0; jn < NT; ++jn) F.b[jn] = gemm_lds_u4(bbase + jn * 16 * 64);
   };
-  // Weight fragments of k-half kh from tile t: row wn*BN/2 + 16 jn + (lane & 15),
-  // chunk (lane >> 4) + 4 kh stored at position chunk ^ (row & 7) = ... ^ (lane & 7).
-  const uint32_t brow = kGemmTiles + (wn * (BN / 2) + (lane & 15)) * kGemmRowBytes;
-  const uint32_t bofs0 = brow + 16 * (((lane >> 4) + 0) ^ (lane & 7));
-  const uint32_t bofs1 = brow + 16 * (((lane >> 4) + 4) ^ (lane & 7));
-  typedef u32x4 BFrags[NT];
-  auto read_b = [&](uint32_t t, int kh, BFrags& F) {
-    const uint32_t base = t * L::kStage + (kh ? bofs1 : bofs0);
+  auto mfma_rows = [&](const Frags& F, int i0) {
 #pragma unroll
-    for (int jn = 0; jn < NT; ++jn) F[jn] = gemm_lds_u4(base + jn * 16 * kGemmRowBytes);
-  };
-  auto mfma_half = [&](const u32x4 (&A)[4], const BFrags& F) {
+    for (int i = i0; i < i0 + 2; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int jn = 0; jn < NT; ++jn) acc[i][jn] = mfma16<kBf16>(A[i], F[jn], acc[i][jn]);
+      for (int jn = 0; jn < NT; ++jn) acc[i][jn] = mfma16<kBf16>(F.a[i], F.b[jn], acc[i][jn]);
   };
 
-  AFrags a0, a1;
-  BFrags fb0, fb1;
-  load_a(0, a0);
-  load_a(1, a1);
-  __syncthreads();  // tables ready
+  // Activations of stage s by DMA into tile abuf: this wave copies row groups
+  // kDma * wave + k (16 rows of 64 bytes each); lane l lands at byte 16 l of
+  // the group, i.e. row (l >> 2), position l & 3, which holds chunk
+  // (l & 3) ^ ((row >> 1) & 3) = (l & 3) ^ ((l >> 3) & 3).  A quad of lanes
+  // reads one row's 64 contiguous bytes.  Rows past m and columns past in_dim
+  // read as zeros (out-of-range offsets).
+  const __amdgpu_buffer_rsrc_t rx = gemm_rsrc(a.x, a.x_records);
+  const uint32_t xkc = (lane & 3) ^ ((lane >> 3) & 3);
+  // (fixed-size arrays: with arrays sized by L::kDma next to the DMA builtin,
+  // hipcc's host pass silently emits no stub for the kernel)
+  uint32_t xsrc[4];
+  bool xok[4];
+  static_assert(L::kDma <= 4, "activation DMA per consumer");
+#pragma unroll
+  for (int k = 0; k < L::kDma; ++k) {
+    const uint32_t row = 16 * (L::kDma * wave + k) + (lane >> 2);
+    xok[k] = m0 + row < a.m;
+    xsrc[k] = ((m0 + row) * a.in_dim + 8 * xkc) * 2;
+  }
+  auto dma_x = [&](uint32_t abuf, uint32_t s) {
+    const bool col_ok = kGemmBK * s + 8 * xkc < a.in_dim;
+#pragma unroll
+    for (int k = 0; k < L::kDma; ++k) {
+      const uint32_t dst = L::kA + abuf * L::kAStage + (L::kDma * wave + k) * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, reinterpret_cast<__attribute__((address_space(3))) void*>(static_cast<uintptr_t>(dst)), 16,
+          (xok[k] && col_ok) ? xsrc[k] + 64 * s : kGemmOutOfRange, 0, 0, 0);
+    }
+  };
+  auto next3 = [](uint32_t b) { return b == 2 ? 0u : b + 1; };
+
+  dma_x(0, 0);
+  dma_x(1, 1);
+  __syncthreads();  // tables ready, activations of stages 0 and 1 in place
   __syncthreads();  // stage 0 published
-  read_b(0, 0, fb0);
-  // Two stages per trip (tiles 0 and 1, activation sets a0 and a1).  Each
-  // stage: read its second k-half, MFMAs of the first half, the barrier that
-  // publishes the next stage, read the next stage's first half, MFMAs of the
-  // second half, then load the activations of the stage two ahead.
-  // sched_barrier keeps the phases in this order.
+  // Stage s: start the DMA of stage s + 2 (its tile, (s + 2) % 3, was last read
+  // before the barrier that published stage s), MFMAs of rows 0-1, the barrier
+  // that publishes stage s + 1 (this wave's DMA of stage s + 1 done), the reads
+  // of stage s + 1 (landing while rows 2-3 of stage s run).  sched_barrier
+  // keeps the phases in this order.
+  Frags f0, f1;
+  uint32_t ab = 0;  // activation tile of stage s
+  read_frags(ab, 0, f0);
   uint32_t s = 0;
   for (; s + 2 < a.nk; s += 2) {
-    read_b(0, 1, fb1);
+    dma_x(next3(next3(ab)), s + 2);
+    mfma_rows(f0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_half(a0.f[0], fb0);
+    consumer_barrier<L::kDma>();
+    ab = next3(ab);
+    read_frags(ab, s + 1, f1);
     __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    read_b(1, 0, fb0);
+    mfma_rows(f0, 2);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_half(a0.f[1], fb1);
+    dma_x(next3(next3(ab)), s + 3);
+    mfma_rows(f1, 0);
     __builtin_amdgcn_sched_barrier(0);
-    load_a(s + 2, a0);
-    read_b(1, 1, fb1);
+    consumer_barrier<L::kDma>();
+    ab = next3(ab);
+    read_frags(ab, s + 2, f0);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_half(a1.f[0], fb0);
+    mfma_rows(f1, 2);
     __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    read_b(0, 0, fb0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_half(a1.f[1], fb1);
-    __builtin_amdgcn_sched_barrier(0);
-    load_a(s + 3, a1);
   }
   // the last one or two stages
-  read_b(0, 1, fb1);
-  mfma_half(a0.f[0], fb0);
-  mfma_half(a0.f[1], fb1);
+  mfma_rows(f0, 0);
+  mfma_rows(f0, 2);
   if (s + 1 < a.nk) {
     __syncthreads();
-    read_b(1, 0, fb0);
-    read_b(1, 1, fb1);
-    mfma_half(a1.f[0], fb0);
-    mfma_half(a1.f[1], fb1);
+    read_frags(next3(ab), s + 1, f1);
+    mfma_rows(f1, 0);
+    mfma_rows(f1, 2);
   }
   // the producers' barriers of the padding stages
   for (uint32_t e = a.nk; e < a.nk_pad; ++e) __syncthreads();
@@ -375,7 +426,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       const float scale = kQ ? a.row_inv[row] : 1.0f;
 #pragma unroll
       for (int jn = 0; jn < NT; ++jn) {
-        const uint32_t col = n0 + wn * (BN / 2) + jn * 16 + (lane & 15);
+        const uint32_t col = n0 + wn * L::TN + jn * 16 + (lane & 15);
         if (col < a.out_dim) {
           float v = acc[i][jn][r];
           if constexpr (kQ) v = v / scale;
@@ -415,8 +466,8 @@ __global__ __launch_bounds__(256) void iq2xxs_quantize_rows_kernel(const uint16_
   }
 }
 
-// The activation fragments are loaded in 16-byte chunks that are wholly in or
-// out of range (in_dim % 8 == 0), and every buffer offset stays below
+// The activations are loaded in 16-byte chunks that are wholly in or out of
+// range (in_dim % 8 == 0), and every buffer offset stays below
 // kGemmOutOfRange.
 bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim) {
   return in_dim % 8 == 0 && (uint64_t)m * in_dim * 2 < kGemmOutOfRange - 4096 &&
@@ -425,21 +476,30 @@ bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim) {
 
 size_t gemm_w8a8_scratch_bytes(uint32_t m, uint32_t in_dim) { return (size_t)m * in_dim * 2; }
 
-template <bool kBf16, int BN, bool kQ>
+template <bool kBf16, int BM, int BN, bool kQ>
 static hipError_t launch_gemm_t(const GemmArgs& a, hipStream_t stream) {
-  using L = GemmLayout<BN>;
+  using L = GemmLayout<BM, BN>;
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
-    hipError_t e =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&iq2xxs_gemm_kernel<kBf16, BN, kQ>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLdsLimit);
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&iq2xxs_gemm_kernel<kBf16, BM, BN, kQ>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLdsLimit);
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
-  dim3 grid((a.out_dim + BN - 1) / BN, (a.m + kGemmBM - 1) / kGemmBM);
-  hipLaunchKernelGGL((iq2xxs_gemm_kernel<kBf16, BN, kQ>), grid, dim3(kGemmThreads), L::kTotal,
-                     stream, a);
+  dim3 grid((a.out_dim + BN - 1) / BN, (a.m + BM - 1) / BM);
+  hipLaunchKernelGGL((iq2xxs_gemm_kernel<kBf16, BM, BN, kQ>), grid, dim3(kGemmThreads),
+                     L::kTotal, stream, a);
   return hipGetLastError();
+}
+
+template <bool kBf16, bool kQ>
+static hipError_t launch_gemm_shape(const GemmArgs& a, hipStream_t stream) {
+  // 256 x 112 tiles halve the dequantisation per CU; used when they still
+  // give most CUs a tile.
+  const uint64_t t256 = (uint64_t)((a.m + 255) / 256) * ((a.out_dim + 111) / 112);
+  if (t256 >= 192) return launch_gemm_t<kBf16, 256, 112, kQ>(a, stream);
+  return launch_gemm_t<kBf16, 128, 128, kQ>(a, stream);
 }
 
 hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
@@ -472,22 +532,12 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
   a.in_dim = in_dim;
   a.bpr = (in_dim + kQK - 1) / kQK;
   a.nk = (in_dim + kGemmBK - 1) / kGemmBK;
-  a.nk_pad = (a.nk + 2 * kGemmGroup - 1) / (2 * kGemmGroup) * (2 * kGemmGroup);
+  a.nk_pad = 1 + (a.nk - 1 + kGemmUnroll - 1) / kGemmUnroll * kGemmUnroll;
   a.x_records = m * in_dim * 2;
   a.wb_records = out_dim * a.bpr * kBytesPerBlock;
   a.ws_records = out_dim * a.bpr * kScalesPerBlock;
-  // tile width: 224 when it fills the CUs better than 128
-  const uint64_t mt = (m + kGemmBM - 1) / kGemmBM;
-  const uint64_t t224 = mt * ((out_dim + 223) / 224), t128 = mt * ((out_dim + 127) / 128);
-  const bool wide = t224 >= 200 || t224 * 224 <= t128 * 128;
-  if (row_inv) {
-    if (wide)
-      return bf ? launch_gemm_t<true, 224, true>(a, stream) : launch_gemm_t<false, 224, true>(a, stream);
-    return bf ? launch_gemm_t<true, 128, true>(a, stream) : launch_gemm_t<false, 128, true>(a, stream);
-  }
-  if (wide)
-    return bf ? launch_gemm_t<true, 224, false>(a, stream) : launch_gemm_t<false, 224, false>(a, stream);
-  return bf ? launch_gemm_t<true, 128, false>(a, stream) : launch_gemm_t<false, 128, false>(a, stream);
+  if (row_inv) return bf ? launch_gemm_shape<true, true>(a, stream) : launch_gemm_shape<false, true>(a, stream);
+  return bf ? launch_gemm_shape<true, false>(a, stream) : launch_gemm_shape<false, false>(a, stream);
 }
 
 }  // namespace cmk
