@@ -339,6 +339,26 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int jn = 0; jn < NT; ++jn) acc[i][jn] = mfma16<kBf16>(F.a[i], F.b[jn], acc[i][jn]);
   };
+  // Rows 2-3 of stage F with the fragment reads of the next stage (into Fn)
+  // interleaved one per MFMA, so that the MFMA pipe restarts right after a
+  // barrier instead of waiting behind the read issue.
+  auto mfma_rows_reading = [&](const Frags& F, uint32_t abuf, uint32_t s_next, Frags& Fn) {
+    const uint32_t abase = aofs + abuf * L::kAStage;
+    const uint32_t bbase = bofs + (s_next & 1) * L::kBStage;
+    int k = 0;
+#pragma unroll
+    for (int i = 2; i < 4; ++i)
+#pragma unroll
+      for (int jn = 0; jn < NT; ++jn) {
+        if (k < 4)
+          Fn.a[k] = gemm_lds_u4(abase + k * 16 * 64);
+        else if (k < 4 + NT)
+          Fn.b[k - 4] = gemm_lds_u4(bbase + (k - 4) * 16 * 64);
+        acc[i][jn] = mfma16<kBf16>(F.a[i], F.b[jn], acc[i][jn]);
+        __builtin_amdgcn_sched_barrier(0);
+        ++k;
+      }
+  };
 
   // Activations of stage s by DMA into tile abuf: this wave copies row groups
   // kDma * wave + k (16 rows of 64 bytes each); lane l lands at byte 16 l of
@@ -370,6 +390,26 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     }
   };
   auto next3 = [](uint32_t b) { return b == 2 ? 0u : b + 1; };
+  // Rows 0-1 of stage F with the DMA instructions of stage s_dma interleaved
+  // one per MFMA.
+  auto mfma_rows_dma = [&](const Frags& F, uint32_t abuf, uint32_t s_dma) {
+    const bool col_ok = kGemmBK * s_dma + 8 * xkc < a.in_dim;
+    int k = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int jn = 0; jn < NT; ++jn) {
+        if (k < L::kDma) {
+          const uint32_t dst = L::kA + abuf * L::kAStage + (L::kDma * wave + k) * 1024;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rx, reinterpret_cast<__attribute__((address_space(3))) void*>(static_cast<uintptr_t>(dst)),
+              16, (xok[k] && col_ok) ? xsrc[k] + 64 * s_dma : kGemmOutOfRange, 0, 0, 0);
+        }
+        acc[i][jn] = mfma16<kBf16>(F.a[i], F.b[jn], acc[i][jn]);
+        __builtin_amdgcn_sched_barrier(0);
+        ++k;
+      }
+  };
 
   dma_x(0, 0);
   dma_x(1, 1);
@@ -385,24 +425,14 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   read_frags(ab, 0, f0);
   uint32_t s = 0;
   for (; s + 2 < a.nk; s += 2) {
-    dma_x(next3(next3(ab)), s + 2);
-    mfma_rows(f0, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    mfma_rows_dma(f0, next3(next3(ab)), s + 2);
     consumer_barrier<L::kDma>();
     ab = next3(ab);
-    read_frags(ab, s + 1, f1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_rows(f0, 2);
-    __builtin_amdgcn_sched_barrier(0);
-    dma_x(next3(next3(ab)), s + 3);
-    mfma_rows(f1, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    mfma_rows_reading(f0, ab, s + 1, f1);
+    mfma_rows_dma(f1, next3(next3(ab)), s + 3);
     consumer_barrier<L::kDma>();
     ab = next3(ab);
-    read_frags(ab, s + 2, f0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma_rows(f1, 2);
-    __builtin_amdgcn_sched_barrier(0);
+    mfma_rows_reading(f1, ab, s + 2, f0);
   }
   // the last one or two stages
   mfma_rows(f0, 0);
