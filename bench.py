@@ -304,7 +304,8 @@ def main():
         "frac_of_hbm_peak": value / HBM_PEAK_GBS,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "cmk::iq2xxs_gemv_kernel<0, true>",
+                     "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false> "
+                               "(XT = 1 for K=4096, 2 for K=14336)",
                      "mean_launch_us": dec["mean_launch_us"],
                      "alg_bytes_per_launch": dec["per_launch_bytes"]},
     }
