@@ -163,20 +163,21 @@ __device__ __forceinline__ float qdq_w8a8(float x, float inv_scale) {
 // Activation digits for the int8 MFMA GEMV.
 //
 // A 32-column chunk of activations with max|x| < 2^e is mapped to integers
-// v = rint(x * 2^(21-e)), |v| <= 2^21.  The rounding is one fma against the
+// v = rint(x * 2^(20-e)), |v| <= 2^20.  The rounding is one fma against the
 // magic constant 1.5*2^23: the sum's mantissa holds 0x400000 + v exactly.
 // u = v + 0x808080 is a 24-bit unsigned value whose bytes b0,b1,b2 give signed
 // digits s_k = b_k - 128 (the bytes of D = u ^ 0x808080 read as int8) with
 //     v = 65536*s2 + 256*s1 + s0      exactly,
 // so sum_k v_k w_k = 65536*C2 + 256*C1 + C0 with C_p = sum_k s_p,k w_k, the
-// three integer dot products the MFMA forms from three digit planes.
-// The chunk scale 2^(e-21) is kept as a float per chunk.
+// three integer dot products the MFMA forms from three digit planes.  Over a
+// 32-column sub-block with |w| <= 43 the sum stays below 32*43*2^20 < 2^31.
+// The chunk scale 2^(e-20) is kept as a float per chunk.
 // ---------------------------------------------------------------------------
-constexpr int kDigitShift = 21;
+constexpr int kDigitShift = 20;
 constexpr float kDigitMagic = 12582912.0f;       // 1.5 * 2^23
 constexpr uint32_t kDigitBias = 0x4ABF7F80u;     // bits(1.5*2^23) - 0x400000 - 0x808080 + 2^32
 
-// Clamp of the chunk exponent so 2^(21-e) and 2^(e-24) stay finite and normal.
+// Clamp of the chunk exponent so 2^(20-e) and 2^(e-23) stay finite and normal.
 __device__ __forceinline__ int digit_exponent(float max_abs) {
   int e;
   (void)frexpf(max_abs, &e);

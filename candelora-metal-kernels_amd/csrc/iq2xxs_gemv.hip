@@ -14,7 +14,7 @@
 //
 // Arithmetic.
 //  * Activations become exact integer digits: each 32-column chunk with
-//    max|x| < 2^e gives v = rint(x*2^(21-e)) split into three signed 8-bit
+//    max|x| < 2^e gives v = rint(x*2^(20-e)) split into three signed 8-bit
 //    digit planes (iq2xxs_device.h), held in LDS.
 //  * Codes expand through two LDS tables: a codebook row holds 16 copies of
 //    {g, -g} (8 magnitude bytes and their negations), a sign row 32 copies of
@@ -24,7 +24,8 @@
 //  * v_mfma_i32_4x4x4_16b_i8: in each of the 16 4x4 blocks the A rows are the
 //    three digit planes (the fourth row is zero) and the B columns are 4 weight
 //    rows; eight instructions give, for 4 rows, the three digit sums of a
-//    32-column sub-block.  The scale d*(2s+1)/8 * 2^(e-21) is applied in fp32.
+//    32-column sub-block, combined exactly in int32 (|sum| < 2^31).  The scale
+//    d*(2s+1)/8 * 2^(e-20) is applied in fp32.
 //  * A wave sums its 16 blocks with DPP and lane-swap moves; the workgroup
 //    adds the slices of a row in slice order.  Results are deterministic.
 //
@@ -37,7 +38,10 @@
 //   2. every wave issues its first two weight tiles;
 //   3. waves 0-7 build the tables, waves 15, 14, ... digitise, everyone stages
 //      the scales; barrier;
-//   4. each wave issues tile k+2 and computes tile k.
+//   4. each wave computes tile k, then issues tile k+2 (issued after the
+//      compute, the load takes a slot the tile just freed instead of stalling
+//      the wave on a full pipeline before it computes).
+// Weight loads carry the nontemporal hint: every code byte is read once.
 // All waves run the same code with the same sequence of loads, so the
 // compiler's count of outstanding loads (s_waitcnt vmcnt) is exact: a wave
 // waits for exactly the load it is about to use.  The first chunk and row are
@@ -75,6 +79,8 @@ constexpr uint32_t kGemvLdsLimit = 160 * 1024;
 constexpr uint32_t kOutOfRange = 0x80000000u;
 // Word 3 of a gfx9 raw buffer resource (32-bit data format, no swizzle).
 constexpr int kBufferWord3 = 0x00020000;
+// Cache policy of the weight loads: nontemporal (read once).
+constexpr int kStreamLoad = 2;
 
 // Table layouts at LDS offset 0.
 //  wide:   [0, 64K)   codebook row e (256 B) = 16 copies of {g lo, g hi, -g lo, -g hi}
@@ -152,6 +158,13 @@ __device__ __forceinline__ u32x4 lds_u4(uint32_t addr) {
 // get the VALU-write -> MFMA-read wait states inserted.
 __device__ __forceinline__ uint32_t bit_select(uint32_t m, uint32_t a, uint32_t b) {
   return (m & a) | (~m & b);
+}
+
+// 65536 c[2] + 256 c[1] + c[0] in 32-bit arithmetic (exact when the result
+// fits in an int32).
+__device__ __forceinline__ int plane_sum(v4i c) {
+  const uint32_t hi = ((uint32_t)c[2] << 8) + (uint32_t)c[1];
+  return (int)((hi << 8) + (uint32_t)c[0]);
 }
 
 // Makes v look modified here (emits no instruction): the decode of a tile's
@@ -294,7 +307,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     const uint32_t pair = slice * kSlicePairs + b;
     const bool ok = k < cnt && row < a.out_dim && pair < a.npairs;
     return __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? row * row_bytes + pair * 16 : kOutOfRange,
-                                                 0, 0);
+                                                 0, kStreamLoad);
   };
   uint32_t sraw[kScaleLoads];
   auto load_scales = [&]() {
@@ -407,7 +420,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   uint32_t cur_slice;
   u32x4 q[kTilesPerWave];
   float acc[kTilesPerWave];
-  float dsc[kTilesPerWave];  // super-block scale d of each tile's (row, pair)
+  float dsc[kTilesPerWave];  // d * 2^-27 of each tile's (row, pair); 0 when out of range
   // d of all of this wave's tiles, from the staged scales (one LDS round trip).
   auto load_tile_scales = [&]() {
     uint32_t slice = t0 / n_rg;
@@ -417,7 +430,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       const uint32_t pair = slice * kSlicePairs + b;
       const uint32_t rl = rgl * 4 + j;
       const bool ok = k < cnt && pair < a.npairs && row_begin + rl < a.out_dim;
-      dsc[k] = ok ? half_bits_to_float(sscale[rl * a.bpr + (pair >> 2)]) : 0.0f;
+      dsc[k] = ok ? half_bits_to_float(sscale[rl * a.bpr + (pair >> 2)]) * 0x1p-27f : 0.0f;
       if (++rgl == n_rg) {
         rgl = 0;
         ++slice;
@@ -478,13 +491,17 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       c[0] = mfma4x4((int)xr[0][kk], (int)w[0][kk], c[0]);
       c[1] = mfma4x4((int)xr[1][kk], (int)w[1][kk], c[1]);
     }
+    // c[h][p] = sum over the 32 columns of digit plane p times w; the exact
+    // integer dot product 65536 c2 + 256 c1 + c0 of a sub-block stays below
+    // 2^31 in magnitude (32 * 43 * 2^20)
+    const float f0 = (float)plane_sum(c[0]);
+    const float f1 = (float)plane_sum(c[1]);
+    // (2s+1) * 2^27 for the sub-block scale s in bits 28-31 of aux_s: the
+    // conversion of s * 2^28 + 2^27 - 1 rounds to (2s+1) * 2^27 exactly
     const float d = dsc[k];
-    // c[h][p] = sum over the 32 columns of digit plane p times w
-    const float f0 = fmaf((float)(c[0][2] * 256 + c[0][1]), 256.0f, (float)c[0][0]);
-    const float f1 = fmaf((float)(c[1][2] * 256 + c[1][1]), 256.0f, (float)c[1][0]);
-    const float coef0 = (float)((words[1] >> 27) | 1u) * (d * xs[0]);
-    const float coef1 = (float)((words[3] >> 27) | 1u) * (d * xs[1]);
-    return fmaf(f1, coef1, f0 * coef0);
+    const float ud0 = (float)((words[1] & 0xF0000000u) | 0x07FFFFFFu) * d;
+    const float ud1 = (float)((words[3] & 0xF0000000u) | 0x07FFFFFFu) * d;
+    return fmaf(f1 * ud1, xs[1], (f0 * ud0) * xs[0]);
   };
   // Row sums of the chunk's tiles for activation row mrow, into out.
   auto reduce_and_store = [&](uint32_t mrow) {
@@ -530,15 +547,16 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   digitize_row(0);
   stage_scales();
   sync();
-  // 4. issue tile k + 2, compute tile k
+  // 4. compute tile k, issue tile k + 2
   load_tile_scales();
   cur_slice = ~0u;
 #pragma unroll
   for (uint32_t k = 0; k < kTilesPerWave; ++k) {
-    if (k + kTilesAhead < kTilesPerWave) q[k + kTilesAhead] = load_tile(k + kTilesAhead);
-    __builtin_amdgcn_sched_barrier(0);
     acc[k] = 0.0f;
     if (k < cnt) acc[k] = compute_tile(k);  // uniform
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + kTilesAhead < kTilesPerWave) q[k + kTilesAhead] = load_tile(k + kTilesAhead);
+    __builtin_amdgcn_sched_barrier(0);
   }
   reduce_and_store(0);
 
