@@ -141,6 +141,8 @@ GEMV_CASES = [
     (3, 13, 300),        # ragged N, partial block
     (1, 6, 41),          # K < one sub-block
     (2, 1028, 28672),    # config 4 down-proj K
+    (1, 28672, 8192),    # config 4 gate/up at M=1: four row chunks per workgroup
+    (1, 8192, 28672),    # config 4 down at M=1: several chunks, digits in more than one round
 ]
 
 
