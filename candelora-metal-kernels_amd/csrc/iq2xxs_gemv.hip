@@ -22,7 +22,7 @@
 //    read is free of bank conflicts.  One v_bitop3 (bit select) per dword
 //    picks g or -g under the mask.
 //  * v_mfma_i32_4x4x4_16b_i8: in each of the 16 4x4 blocks the A rows are the
-//    three digit planes (the fourth row is zero) and the B columns are 4 weight
+//    three digit planes (the fourth row is unused) and the B columns are 4 weight
 //    rows; eight instructions give, for 4 rows, the three digit sums of a
 //    32-column sub-block, combined exactly in int32 (|sum| < 2^31).  The scale
 //    d*(2s+1)/8 * 2^(e-20) is applied in fp32.
@@ -246,6 +246,8 @@ struct GemvArgs {
   float* out;
   uint32_t m, out_dim, in_dim;
   uint32_t bpr;           // super-blocks per row
+  uint32_t spr;           // staged scales per row: bpr rounded up to whole slices
+  uint32_t spr_magic;     // ceil(2^32 / spr): i / spr = umulhi(i, spr_magic) for i < 2^16
   uint32_t npairs;        // sub-block pairs per row = 4 * bpr
   uint32_t nslices;       // tiles per row group = ceil(npairs / 16)
   uint32_t rg_per_chunk;  // row groups per chunk
@@ -299,32 +301,40 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     cnt = base + (wave < extra ? 1u : 0u);
     t0 = wave * base + min(wave, extra);
   };
+  // Lane (b, j) loads pair b of row j of the tile: byte offset
+  // (first row of the tile's row group) * row_bytes + slice * 256 (uniform)
+  // plus j * row_bytes + 16 b (this lane's constant).  Rows past out_dim lie
+  // past the buffer's end and read zeros; pairs past the row end read other
+  // codes, whose staged scale d is 0; tiles past this wave's count are sent
+  // past the buffer.
+  const uint32_t tile_lane_ofs = j * row_bytes + 16 * b;
   auto load_tile = [&](uint32_t k) -> u32x4 {
     const uint32_t tau = t0 + k;
     const uint32_t slice = tau / n_rg;
     const uint32_t rgl = tau - slice * n_rg;
-    const uint32_t row = row_begin + rgl * 4 + j;
-    const uint32_t pair = slice * kSlicePairs + b;
-    const bool ok = k < cnt && row < a.out_dim && pair < a.npairs;
-    return __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? row * row_bytes + pair * 16 : kOutOfRange,
-                                                 0, kStreamLoad);
+    const uint32_t base = k < cnt ? (row_begin + rgl * 4) * row_bytes + slice * (kSlicePairs * 16)
+                                  : kOutOfRange;  // uniform
+    return __builtin_amdgcn_raw_buffer_load_b128(rw, base + tile_lane_ofs, 0, kStreamLoad);
   };
+  // Super-block scales of the chunk, staged as rows of a.spr entries (blocks
+  // padded to whole slices) with zeros for padding rows and blocks.
   uint32_t sraw[kScaleLoads];
   auto load_scales = [&]() {
-    const uint32_t nscales = rows * a.bpr;
 #pragma unroll
     for (uint32_t k = 0; k < kScaleLoads; ++k) {
       const uint32_t i = tid + k * kGemvThreads;
+      const uint32_t rl = __umulhi(i, a.spr_magic), blk = i - rl * a.spr;  // i / spr, exact
+      const bool ok = rl < rows && blk < a.bpr;
       sraw[k] = __builtin_amdgcn_raw_buffer_load_b16(
-          rs, i < nscales ? (row_begin * a.bpr + i) * kScalesPerBlock : kOutOfRange, 0, 0);
+          rs, ok ? ((row_begin + rl) * a.bpr + blk) * kScalesPerBlock : kOutOfRange, 0, 0);
     }
   };
   auto stage_scales = [&]() {
-    const uint32_t nscales = rows * a.bpr;
+    const uint32_t nstaged = a.rg_per_chunk * 4 * a.spr;
 #pragma unroll
     for (uint32_t k = 0; k < kScaleLoads; ++k) {
       const uint32_t i = tid + k * kGemvThreads;
-      if (i < nscales) sscale[i] = (uint16_t)sraw[k];
+      if (i < nstaged) sscale[i] = (uint16_t)sraw[k];
     }
   };
 
@@ -415,22 +425,27 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // ---- dot products of one tile
   const uint32_t cg = 16 * (lane & (TL::kGridCopies - 1));  // this lane's codebook copy
   const uint32_t cs = TL::kSignBase + 8 * (lane & (TL::kSignCopies - 1));
-  uint32_t xr[2][8];  // digit plane j of the tile's two sub-blocks (j = 3: zero)
+  // Digit plane of this lane's A row.  Lanes with j = 3 load plane 2 as well:
+  // A row 3 only feeds C row 3, which is never read, so its contents do not
+  // matter and the reload needs no branch.
+  const uint32_t plane = min(j, 2u);
+  uint32_t xr[2][8];  // digit plane of the tile's two sub-blocks
   float xs[2];        // their chunk scales
   uint32_t cur_slice;
   u32x4 q[kTilesPerWave];
   float acc[kTilesPerWave];
   float dsc[kTilesPerWave];  // d * 2^-27 of each tile's (row, pair); 0 when out of range
   // d of all of this wave's tiles, from the staged scales (one LDS round trip).
+  // Staged entry of (row j, pair b): (rgl * 4) * spr + slice * 4 (uniform)
+  // plus j * spr + b / 4 (this lane's constant).
+  const uint32_t scale_lane_ofs = j * a.spr + (b >> 2);
   auto load_tile_scales = [&]() {
     uint32_t slice = t0 / n_rg;
     uint32_t rgl = t0 - slice * n_rg;
 #pragma unroll
     for (uint32_t k = 0; k < kTilesPerWave; ++k) {
-      const uint32_t pair = slice * kSlicePairs + b;
-      const uint32_t rl = rgl * 4 + j;
-      const bool ok = k < cnt && pair < a.npairs && row_begin + rl < a.out_dim;
-      dsc[k] = ok ? half_bits_to_float(sscale[rl * a.bpr + (pair >> 2)]) * 0x1p-27f : 0.0f;
+      const uint32_t base = rgl * 4 * a.spr + slice * (kSlicePairs / 4);  // uniform
+      dsc[k] = k < cnt ? half_bits_to_float(sscale[base + scale_lane_ofs]) * 0x1p-27f : 0.0f;
       if (++rgl == n_rg) {
         rgl = 0;
         ++slice;
@@ -440,23 +455,18 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // This lane's partial of tile k (before the sum over the 16 blocks).
   auto compute_tile = [&](uint32_t k) -> float {
     const uint32_t slice = (t0 + k) / n_rg;
-    const uint32_t pair = slice * kSlicePairs + b;
-    const bool pair_ok = pair < a.npairs;
     if (slice != cur_slice) {  // uniform
       cur_slice = slice;
+      // a pair past the row end reads the last pair's digits: its d is 0
+      const uint32_t pair = min(slice * kSlicePairs + b, a.npairs - 1);
 #pragma unroll
       for (uint32_t h = 0; h < 2; ++h) {
         const uint32_t sb = 2 * pair + h;
-        xs[h] = pair_ok ? xsc[sb] : 0.0f;
-        if (pair_ok && j < 3) {
-          const u32x4* src = reinterpret_cast<const u32x4*>(xdig + j * a.plane_stride + sb * 32);
-          const u32x4 lo = src[0], hi = src[1];
-          xr[h][0] = lo.x; xr[h][1] = lo.y; xr[h][2] = lo.z; xr[h][3] = lo.w;
-          xr[h][4] = hi.x; xr[h][5] = hi.y; xr[h][6] = hi.z; xr[h][7] = hi.w;
-        } else {
-#pragma unroll
-          for (int kk = 0; kk < 8; ++kk) xr[h][kk] = 0u;
-        }
+        xs[h] = xsc[sb];
+        const u32x4* src = reinterpret_cast<const u32x4*>(xdig + plane * a.plane_stride + sb * 32);
+        const u32x4 lo = src[0], hi = src[1];
+        xr[h][0] = lo.x; xr[h][1] = lo.y; xr[h][2] = lo.z; xr[h][3] = lo.w;
+        xr[h][4] = hi.x; xr[h][5] = hi.y; xr[h][6] = hi.z; xr[h][7] = hi.w;
       }
     }
     if constexpr (kMulti) pin_here(q[k]);
@@ -631,8 +641,9 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   // as few chunks per workgroup as the tile budget allows, evenly sized
   const uint64_t per_wg_chunks = (target + rg_per_chunk - 1) / rg_per_chunk;
   rg_per_chunk = (target + per_wg_chunks - 1) / per_wg_chunks;
-  if (rg_per_chunk * 4 * bpr > (uint64_t)kScaleLoads * kGemvThreads) {
-    rg_per_chunk = (kScaleLoads * kGemvThreads) / (4 * bpr);
+  const uint64_t spr = nslices * (kSlicePairs / 4);  // staged scales per row
+  if (rg_per_chunk * 4 * spr > (uint64_t)kScaleLoads * kGemvThreads) {
+    rg_per_chunk = (kScaleLoads * kGemvThreads) / (4 * spr);
     if (rg_per_chunk < 1) return false;
   }
   p->nslices = (uint32_t)nslices;
@@ -644,7 +655,7 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   // longer rows digitise in further rounds
   p->xt = p->ntasks <= kGemvThreads ? 1 : 2;
   p->plane_stride = (uint32_t)(nsb * 32 + 16);
-  const uint64_t scale_bytes = align16(rg_per_chunk * 4 * bpr * 2);
+  const uint64_t scale_bytes = align16(rg_per_chunk * 4 * nslices * (kSlicePairs / 4) * 2);
   const uint64_t rest = scale_bytes + align16(nsb * 4) + 3ull * p->plane_stride +
                         align16(rg_per_chunk * nslices * 16) + kGemvWaves * 4;
   p->wide = GemvTables<true>::kBytes + rest <= kGemvLdsLimit;
@@ -719,6 +730,8 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
   a.out_dim = out_dim;
   a.in_dim = in_dim;
   a.bpr = (in_dim + kQK - 1) / kQK;
+  a.spr = p.nslices * (kSlicePairs / 4);
+  a.spr_magic = (uint32_t)((0x100000000ull + a.spr - 1) / a.spr);
   a.npairs = a.bpr * 4;
   a.nslices = p.nslices;
   a.rg_per_chunk = p.rg_per_chunk;
