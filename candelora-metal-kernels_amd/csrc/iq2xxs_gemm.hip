@@ -19,15 +19,16 @@
 // stages of 32 columns (one 32-weight sub-block of every weight row).  For
 // m = 512, n = 14336 the tile is 256 x 112: 2 x 128 = 256 workgroups, one per
 // CU, and every weight sub-block is dequantised by two CUs only.
-//  * Waves 0-3 (consumers) each own a 64 x BN/WN block of the tile.  They read
-//    fragments from LDS, issue MFMAs, and copy the activations of the stage two
-//    ahead into LDS with global-to-LDS DMA (buffer_load ... lds), which costs
-//    them no VALU work: on gfx950 a wave's VALU work does not overlap its own
-//    MFMAs, while VALU work of another wave on the same SIMD does.
+//  * Waves 0-3 (consumers) each own a 64 x BN/WN block of the tile.  They only
+//    read fragments from LDS and issue MFMAs: on gfx950 a wave's VALU work and
+//    memory-issue stalls do not overlap its own MFMAs, while work of another
+//    wave on the same SIMD does.
 //  * Waves 4-7 (producers) dequantise the weights: two lanes per weight row,
 //    two 8-weight groups each per stage, with the table reads of the next
-//    stage in flight while the current one is assembled.  A barrier per stage
-//    publishes it.
+//    stage in flight while the current one is assembled.  They also copy the
+//    activations of the next stage into a triple-buffered LDS tile with
+//    global-to-LDS DMA (buffer_load ... lds).  A barrier per stage publishes
+//    it.
 // Layout and load shapes follow measurements on gfx950: vector loads run at
 // full rate only when each quad of lanes reads 64 contiguous bytes; LDS reads
 // run at about 270 B/clk per CU when conflict-free, writes at about 100 B/clk;
@@ -139,15 +140,14 @@ struct GemmArgs {
   uint32_t x_records, wb_records, ws_records;
 };
 
-// Barrier of the consumer waves inside the main loop: waits until at most
-// kVm of this wave's DMAs are in flight and its LDS reads are done, then
-// s_barrier, without a memory fence (a workgroup fence would also wait for
-// the DMA of the stage after next).  The producers' side of every barrier is
-// a full __syncthreads, so their LDS writes are complete before it.  The
-// memory clobber keeps the compiler from moving LDS accesses across it.
+// Barrier of the main loop without a memory fence: waits until at most kVm of
+// this wave's vector-memory operations are in flight and its LDS accesses are
+// done, then s_barrier.  A workgroup fence would also wait for the activation
+// DMA of the next stage, which is meant to stay in flight.  The memory clobber
+// keeps the compiler from moving LDS accesses across it.
 template <int kVm>
-__device__ __forceinline__ void consumer_barrier() {
-  static_assert(kVm >= 0 && kVm < 16, "vmcnt field");
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(kVm >= 0 && kVm < 64, "vmcnt field");
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kVm) : "memory");
 }
 
@@ -265,12 +265,47 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       aux_s = (sb & 1) ? q.w : q.y;
     };
 
+    // Activations of stage s by DMA into tile s % 3: producer wave pw copies
+    // row groups kDma * pw + k (16 rows of 64 bytes each); lane l lands at
+    // byte 16 l of the group, i.e. row (l >> 2), position l & 3, which holds
+    // chunk (l & 3) ^ ((row >> 1) & 3) = (l & 3) ^ ((l >> 3) & 3).  A quad of
+    // lanes reads one row's 64 contiguous bytes.  Rows past m and columns past
+    // in_dim read as zeros (out-of-range offsets).
+    const uint32_t pw = wave - 4;
+    const __amdgpu_buffer_rsrc_t rx = gemm_rsrc(a.x, a.x_records);
+    const uint32_t xkc = (lane & 3) ^ ((lane >> 3) & 3);
+    // (fixed-size arrays: with arrays sized by L::kDma next to the DMA builtin,
+    // hipcc's host pass silently emits no stub for the kernel)
+    uint32_t xsrc[4];
+    bool xok[4];
+    static_assert(L::kDma <= 4, "activation DMA per producer");
+#pragma unroll
+    for (int k = 0; k < L::kDma; ++k) {
+      const uint32_t row = 16 * (L::kDma * pw + k) + (lane >> 2);
+      xok[k] = m0 + row < a.m;
+      xsrc[k] = ((m0 + row) * a.in_dim + 8 * xkc) * 2;
+    }
+    auto dma_x = [&](uint32_t s) {
+      const bool col_ok = kGemmBK * s + 8 * xkc < a.in_dim;
+      const uint32_t abuf = s % 3;
+#pragma unroll
+      for (int k = 0; k < L::kDma; ++k) {
+        const uint32_t dst = L::kA + abuf * L::kAStage + (L::kDma * pw + k) * 1024;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rx, reinterpret_cast<__attribute__((address_space(3))) void*>(static_cast<uintptr_t>(dst)),
+            16, (xok[k] && col_ok) ? xsrc[k] + 64 * s : kGemmOutOfRange, 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
     Codes c0, c1;
     Tables t0, t1;
     load_codes(0, c0);
     load_codes(1, c1);
+    dma_x(0);
     __syncthreads();  // tables ready
-    // prologue: stage 0, and the table reads of stage 1
+    // prologue: stage 0, the activations of stage 1, and the table reads of stage 1
+    dma_x(1);
     {
       uint32_t g0, s0v, g1, s1v;
       aux_of(c0, 0, g0, s0v);
@@ -279,18 +314,23 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       read_tables(g1, s1v, t1);
       write_w(0, s0v, c0.d, t0);
     }
-    __syncthreads();  // stage 0 published
-    // Step s reads the tables of stage s + 1, writes stage s (weight tile
-    // s & 1) from the tables read one step earlier, and after the last stage
-    // of a block reloads that code set with the block two ahead.  A trip
-    // covers kGemmUnroll steps from s0 = 1 (mod 16), so every set choice below
-    // is a compile-time constant and the body is one straight-line sequence
-    // (exact wait counts).
+    __syncthreads();  // stage 0 published (with its activations)
+    // Step s starts the DMA of the activations of stage s + 1 (their tile,
+    // (s + 1) % 3, was last read before the previous barrier), reads the
+    // tables of stage s + 1, writes stage s (weight tile s & 1) from the
+    // tables read one step earlier, and after the last stage of a block
+    // reloads that code set with the block two ahead.  Its barrier publishes
+    // stage s: the DMA of stage s (issued one step earlier) must have landed,
+    // while the DMA of stage s + 1 and code loads may stay in flight.  A trip
+    // covers kGemmUnroll steps from s0 = 1 (mod 16), so every set choice and
+    // wait count below is a compile-time constant and the body is one
+    // straight-line sequence (exact wait counts).
     for (uint32_t s0 = 1; s0 < a.nk_pad; s0 += kGemmUnroll) {
 #pragma unroll
       for (int j = 0; j < kGemmUnroll; ++j) {
         const uint32_t s = s0 + j;
         const int cj = 1 + j;  // s modulo 16
+        dma_x(s + 1);
         Codes& cc = ((cj >> 3) & 1) ? c1 : c0;        // block of stage s
         Codes& cn = (((cj + 1) >> 3) & 1) ? c1 : c0;  // block of stage s + 1
         Tables& tc = (cj & 1) ? t1 : t0;
@@ -301,7 +341,14 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
         aux_of(cc, cj & 7, gc, sc);
         write_w((uint32_t)(cj & 1), sc, cc.d, tc);
         if ((cj & 7) == 7) load_codes((s >> 3) + 2, cc);
-        __syncthreads();
+        // in flight after the DMA of stage s: code loads of step s - 1, the
+        // DMA of stage s + 1, code loads of step s (5 loads per code set; at
+        // most one of the two steps loads codes).  cj is a constant once the
+        // loop is unrolled, so one branch remains.
+        if (((cj - 1) & 7) == 7 || (cj & 7) == 7)
+          stage_barrier<L::kDma + 5>();
+        else
+          stage_barrier<L::kDma>();
       }
     }
     return;
@@ -360,77 +407,34 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       }
   };
 
-  // Activations of stage s by DMA into tile abuf: this wave copies row groups
-  // kDma * wave + k (16 rows of 64 bytes each); lane l lands at byte 16 l of
-  // the group, i.e. row (l >> 2), position l & 3, which holds chunk
-  // (l & 3) ^ ((row >> 1) & 3) = (l & 3) ^ ((l >> 3) & 3).  A quad of lanes
-  // reads one row's 64 contiguous bytes.  Rows past m and columns past in_dim
-  // read as zeros (out-of-range offsets).
-  const __amdgpu_buffer_rsrc_t rx = gemm_rsrc(a.x, a.x_records);
-  const uint32_t xkc = (lane & 3) ^ ((lane >> 3) & 3);
-  // (fixed-size arrays: with arrays sized by L::kDma next to the DMA builtin,
-  // hipcc's host pass silently emits no stub for the kernel)
-  uint32_t xsrc[4];
-  bool xok[4];
-  static_assert(L::kDma <= 4, "activation DMA per consumer");
-#pragma unroll
-  for (int k = 0; k < L::kDma; ++k) {
-    const uint32_t row = 16 * (L::kDma * wave + k) + (lane >> 2);
-    xok[k] = m0 + row < a.m;
-    xsrc[k] = ((m0 + row) * a.in_dim + 8 * xkc) * 2;
-  }
-  auto dma_x = [&](uint32_t abuf, uint32_t s) {
-    const bool col_ok = kGemmBK * s + 8 * xkc < a.in_dim;
-#pragma unroll
-    for (int k = 0; k < L::kDma; ++k) {
-      const uint32_t dst = L::kA + abuf * L::kAStage + (L::kDma * wave + k) * 1024;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, reinterpret_cast<__attribute__((address_space(3))) void*>(static_cast<uintptr_t>(dst)), 16,
-          (xok[k] && col_ok) ? xsrc[k] + 64 * s : kGemmOutOfRange, 0, 0, 0);
-    }
-  };
   auto next3 = [](uint32_t b) { return b == 2 ? 0u : b + 1; };
-  // Rows 0-1 of stage F with the DMA instructions of stage s_dma interleaved
-  // one per MFMA.
-  auto mfma_rows_dma = [&](const Frags& F, uint32_t abuf, uint32_t s_dma) {
-    const bool col_ok = kGemmBK * s_dma + 8 * xkc < a.in_dim;
-    int k = 0;
+  // Rows 0-1 of stage F, one MFMA after another.
+  auto mfma_rows01 = [&](const Frags& F) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int jn = 0; jn < NT; ++jn) {
-        if (k < L::kDma) {
-          const uint32_t dst = L::kA + abuf * L::kAStage + (L::kDma * wave + k) * 1024;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rx, reinterpret_cast<__attribute__((address_space(3))) void*>(static_cast<uintptr_t>(dst)),
-              16, (xok[k] && col_ok) ? xsrc[k] + 64 * s_dma : kGemmOutOfRange, 0, 0, 0);
-        }
         acc[i][jn] = mfma16<kBf16>(F.a[i], F.b[jn], acc[i][jn]);
         __builtin_amdgcn_sched_barrier(0);
-        ++k;
       }
   };
 
-  dma_x(0, 0);
-  dma_x(1, 1);
-  __syncthreads();  // tables ready, activations of stages 0 and 1 in place
+  __syncthreads();  // tables ready
   __syncthreads();  // stage 0 published
-  // Stage s: start the DMA of stage s + 2 (its tile, (s + 2) % 3, was last read
-  // before the barrier that published stage s), MFMAs of rows 0-1, the barrier
-  // that publishes stage s + 1 (this wave's DMA of stage s + 1 done), the reads
-  // of stage s + 1 (landing while rows 2-3 of stage s run).  sched_barrier
-  // keeps the phases in this order.
+  // Stage s: MFMAs of rows 0-1, the barrier that publishes stage s + 1, the
+  // reads of stage s + 1 (landing while rows 2-3 of stage s run).
+  // sched_barrier keeps the phases in this order.
   Frags f0, f1;
   uint32_t ab = 0;  // activation tile of stage s
   read_frags(ab, 0, f0);
   uint32_t s = 0;
   for (; s + 2 < a.nk; s += 2) {
-    mfma_rows_dma(f0, next3(next3(ab)), s + 2);
-    consumer_barrier<L::kDma>();
+    mfma_rows01(f0);
+    stage_barrier<0>();
     ab = next3(ab);
     mfma_rows_reading(f0, ab, s + 1, f1);
-    mfma_rows_dma(f1, next3(next3(ab)), s + 3);
-    consumer_barrier<L::kDma>();
+    mfma_rows01(f1);
+    stage_barrier<0>();
     ab = next3(ab);
     mfma_rows_reading(f1, ab, s + 2, f0);
   }
