@@ -198,9 +198,11 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   if (wave >= 4) {
     // ======== producers: lanes 2r, 2r + 1 own weight row n0 + r ========
     const uint32_t p = tid - kGemmProducer0;  // 0..255
-    const uint32_t r = p >> 1, h = p & 1;     // row, group pair (groups 2h, 2h + 1)
-    const bool active = r < (uint32_t)BN;
-    const bool row_ok = active && n0 + r < a.out_dim;
+    // row, group pair (groups 2h, 2h + 1).  When 2 * BN < 256 the lanes past
+    // the tile redo rows 0.. (same loads, same values written to the same
+    // place), which keeps every lane on the same branch-free path.
+    const uint32_t r = (p >> 1) % (uint32_t)BN, h = p & 1;
+    const bool row_ok = n0 + r < a.out_dim;
     const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(a.wb, a.wb_records);
     const __amdgpu_buffer_rsrc_t rs = gemm_rsrc(a.ws, a.ws_records);
     const uint32_t row_blk = (n0 + r) * a.bpr;
@@ -234,7 +236,6 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       u32x4 sel[2], sgn[2];
     };
     auto read_tables = [&](uint32_t aux_g, uint32_t aux_s, Tables& T) {
-      if (!active) return;
 #pragma unroll
       for (int gg = 0; gg < 2; ++gg) {
         const uint32_t g = 2 * h + gg;
@@ -244,7 +245,6 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       }
     };
     auto write_w = [&](uint32_t t, uint32_t aux_s, uint32_t dbits, const Tables& T) {
-      if (!active) return;
       // exact fp32 level values l * d * (2s + 1) / 8, then one rounding each
       const float tdf = half_bits_to_float((uint16_t)dbits) * (float)((aux_s >> 27) | 1u) * 0.125f;
       const uint32_t pool_lo = pack2<kBf16>(8.0f * tdf, 25.0f * tdf);
