@@ -24,11 +24,11 @@
 //    memory-issue stalls do not overlap its own MFMAs, while work of another
 //    wave on the same SIMD does.
 //  * Waves 4-7 (producers) dequantise the weights: two lanes per weight row,
-//    two 8-weight groups each per stage, with the table reads of the next
-//    stage in flight while the current one is assembled.  They also copy the
-//    activations of the next stage into a triple-buffered LDS tile with
-//    global-to-LDS DMA (buffer_load ... lds).  A barrier per stage publishes
-//    it.
+//    two 8-weight groups each per stage; the table reads of the next stage
+//    are issued after the current stage is written and stay in flight across
+//    the barrier.  They also copy the activations two stages ahead into four
+//    rotating LDS tiles with global-to-LDS DMA (buffer_load ... lds).  A
+//    barrier per stage publishes it.
 // Layout and load shapes follow measurements on gfx950: vector loads run at
 // full rate only when each quad of lanes reads 64 contiguous bytes; LDS reads
 // run at about 270 B/clk per CU when conflict-free, writes at about 100 B/clk;
@@ -37,8 +37,10 @@
 //
 // LDS layout (64 KB aligned tables, so one v_perm forms a selector address):
 //   [0, 64K)      selector table: 256 codebook entries x 16 copies x 16 B
-//   [64K, 96K)    sign table: 128 sign indices x 16 copies x 16 B
-//   [96K, ...)    three activation tiles (BM rows x 64 B), then two weight
+//                 (lane l reads copy l & 15: conflict-free)
+//   [64K, 80K)    sign table: 128 sign indices x 8 copies x 16 B (lane l
+//                 reads copy l & 7; lanes l and l + 8 may meet in a bank)
+//   [80K, ...)    four activation tiles (BM rows x 64 B), then two weight
 //                 tiles (BN rows x 64 B); 16-byte chunk c of row r is stored
 //                 at position c ^ ((r >> 1) & 3), which makes the MFMA
 //                 fragment reads conflict-free.
@@ -69,7 +71,8 @@ constexpr int kGemmProducer0 = 256;          // first producer thread
 constexpr int kGemmUnroll = 16;              // producer steps per loop trip
 constexpr uint32_t kGemmSel = 0;             // selector table
 constexpr uint32_t kGemmSign = 0x10000;      // sign table
-constexpr uint32_t kGemmTiles = 0x18000;     // activation and weight tiles
+constexpr uint32_t kGemmSignCopies = 8;
+constexpr uint32_t kGemmTiles = 0x14000;     // activation and weight tiles
 constexpr uint32_t kGemmLdsLimit = 160 * 1024;
 constexpr uint32_t kGemmOutOfRange = 0x80000000u;
 constexpr int kGemmBufferWord3 = 0x00020000;
@@ -81,10 +84,10 @@ struct GemmLayout {
   static constexpr int NT = TN / 16;                  // 16-wide MFMA tiles per consumer in n
   static constexpr uint32_t kAStage = BM * 64;        // one activation tile
   static constexpr uint32_t kBStage = BN * 64;        // one weight tile
-  static constexpr uint32_t kA = kGemmTiles;          // three activation tiles
-  static constexpr uint32_t kB = kA + 3 * kAStage;    // two weight tiles
+  static constexpr uint32_t kA = kGemmTiles;          // four activation tiles
+  static constexpr uint32_t kB = kA + 4 * kAStage;    // two weight tiles
   static constexpr uint32_t kTotal = kB + 2 * kBStage;
-  static constexpr int kDma = BM / 64;                // DMA instructions per consumer per stage
+  static constexpr int kDma = BM / 64;                // DMA instructions per producer wave per stage
   static_assert(WM * WN == 4 && TN % 16 == 0, "four consumer waves of whole MFMA tiles");
   static_assert(2 * BN <= 256, "two producer lanes per weight row");
   static_assert(kTotal <= kGemmLdsLimit, "LDS budget");
@@ -141,18 +144,20 @@ struct GemmArgs {
 };
 
 // Barrier of the main loop without a memory fence: waits until at most kVm of
-// this wave's vector-memory operations are in flight and its LDS accesses are
-// done, then s_barrier.  A workgroup fence would also wait for the activation
-// DMA of the next stage, which is meant to stay in flight.  The memory clobber
-// keeps the compiler from moving LDS accesses across it.
-template <int kVm>
+// this wave's vector-memory operations and at most kLgkm of its LDS accesses
+// are in flight (both complete in issue order), then s_barrier.  A workgroup
+// fence would also wait for the activation DMA of later stages, which is
+// meant to stay in flight.  The memory clobber keeps the compiler from moving
+// LDS accesses across it.
+template <int kVm, int kLgkm = 0>
 __device__ __forceinline__ void stage_barrier() {
-  static_assert(kVm >= 0 && kVm < 64, "vmcnt field");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kVm) : "memory");
+  static_assert(kVm >= 0 && kVm < 64 && kLgkm >= 0 && kLgkm < 16, "waitcnt fields");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(%1)\n\ts_barrier" ::"n"(kVm), "n"(kLgkm) : "memory");
 }
 
-// Builds the selector and sign tables (16 copies each) with the workgroup's
-// 512 threads: 256 selector entries and 128 sign entries, one per thread.
+// Builds the selector table (16 copies) and the sign table (8 copies) with the
+// workgroup's 512 threads: 256 selector entries and 128 sign entries, one per
+// thread.
 __device__ __forceinline__ void build_gemm_tables(uint32_t tid) {
   if (tid >= 256 + 128) return;
   u32x4 v;
@@ -176,7 +181,11 @@ __device__ __forceinline__ void build_gemm_tables(uint32_t tid) {
     for (int p = 0; p < 4; ++p)
       w[p] = (((s >> (2 * p)) & 1u) ? 0x8000u : 0u) | (((s >> (2 * p + 1)) & 1u) ? 0x80000000u : 0u);
     v = u32x4{w[0], w[1], w[2], w[3]};
-    base = kGemmSign + i * 256;
+    base = kGemmSign + i * (16 * kGemmSignCopies);
+#pragma unroll
+    for (uint32_t k = 0; k < kGemmSignCopies; ++k)
+      gemm_lds_store(base + 16 * ((k + i) & (kGemmSignCopies - 1)), v);
+    return;
   }
 #pragma unroll
   for (uint32_t k = 0; k < 16; ++k) gemm_lds_store(base + 16 * ((k + tid) & 15), v);
@@ -206,7 +215,8 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(a.wb, a.wb_records);
     const __amdgpu_buffer_rsrc_t rs = gemm_rsrc(a.ws, a.ws_records);
     const uint32_t row_blk = (n0 + r) * a.bpr;
-    const uint32_t cs = 16 * (lane & 15);  // table copy of this lane
+    const uint32_t cs = 16 * (lane & 15);  // selector-table copy of this lane
+    const uint32_t css = 16 * (lane & (kGemmSignCopies - 1));  // sign-table copy
     const uint32_t wdst0 = L::kB + r * 64 + 16 * ((2 * h + 0) ^ ((r >> 1) & 3));
     const uint32_t wdst1 = L::kB + r * 64 + 16 * ((2 * h + 1) ^ ((r >> 1) & 3));
 
@@ -231,7 +241,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     };
     // Dequantisation of this lane's two groups of a sub-block, in two parts:
-    // the table reads, then the assembly into weight tile t (one stage apart).
+    // the table reads, then the assembly into weight tile t (one step later).
     struct Tables {
       u32x4 sel[2], sgn[2];
     };
@@ -241,7 +251,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
         const uint32_t g = 2 * h + gg;
         // selector entry aux_g.byte(g): address (e << 8) | cs in one v_perm
         T.sel[gg] = gemm_lds_u4(kGemmSel + __builtin_amdgcn_perm(aux_g, cs, 0x0C0C0000u | ((4u + g) << 8)));
-        T.sgn[gg] = gemm_lds_u4(kGemmSign + (__builtin_amdgcn_ubfe(aux_s, 7 * g, 7) << 8) + cs);
+        T.sgn[gg] = gemm_lds_u4(kGemmSign + __builtin_amdgcn_ubfe(aux_s, 7 * g, 7) * (16 * kGemmSignCopies) + css);
       }
     };
     auto write_w = [&](uint32_t t, uint32_t aux_s, uint32_t dbits, const Tables& T) {
@@ -265,7 +275,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       aux_s = (sb & 1) ? q.w : q.y;
     };
 
-    // Activations of stage s by DMA into tile s % 3: producer wave pw copies
+    // Activations of stage s by DMA into tile s & 3: producer wave pw copies
     // row groups kDma * pw + k (16 rows of 64 bytes each); lane l lands at
     // byte 16 l of the group, i.e. row (l >> 2), position l & 3, which holds
     // chunk (l & 3) ^ ((row >> 1) & 3) = (l & 3) ^ ((l >> 3) & 3).  A quad of
@@ -287,7 +297,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     }
     auto dma_x = [&](uint32_t s) {
       const bool col_ok = kGemmBK * s + 8 * xkc < a.in_dim;
-      const uint32_t abuf = s % 3;
+      const uint32_t abuf = s & 3;
 #pragma unroll
       for (int k = 0; k < L::kDma; ++k) {
         const uint32_t dst = L::kA + abuf * L::kAStage + (L::kDma * pw + k) * 1024;
@@ -304,8 +314,10 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     load_codes(1, c1);
     dma_x(0);
     __syncthreads();  // tables ready
-    // prologue: stage 0, the activations of stage 1, and the table reads of stage 1
+    // prologue: stage 0, the activations of stages 1 and 2, and the table
+    // reads of stage 1
     dma_x(1);
+    dma_x(2);
     {
       uint32_t g0, s0v, g1, s1v;
       aux_of(c0, 0, g0, s0v);
@@ -315,13 +327,15 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       write_w(0, s0v, c0.d, t0);
     }
     __syncthreads();  // stage 0 published (with its activations)
-    // Step s starts the DMA of the activations of stage s + 1 (their tile,
-    // (s + 1) % 3, was last read before the previous barrier), reads the
-    // tables of stage s + 1, writes stage s (weight tile s & 1) from the
-    // tables read one step earlier, and after the last stage of a block
-    // reloads that code set with the block two ahead.  Its barrier publishes
-    // stage s: the DMA of stage s (issued one step earlier) must have landed,
-    // while the DMA of stage s + 1 and code loads may stay in flight.  A trip
+    // Step s starts the DMA of the activations of stage s + 2 (their tile,
+    // (s + 2) & 3, held stage s - 2, whose fragments were read before the
+    // previous barrier), writes stage s (weight tile s & 1) from the tables
+    // read one step earlier, then reads the tables of stage s + 1, and after
+    // the last stage of a block reloads that code set with the block two
+    // ahead.  Its barrier publishes stage s: the weight writes must be done
+    // (the four table reads issued after them may stay in flight), and the
+    // DMA of stage s (issued two steps earlier) must have landed while the
+    // DMA of stages s + 1 and s + 2 and code loads may stay in flight.  A trip
     // covers kGemmUnroll steps from s0 = 1 (mod 16), so every set choice and
     // wait count below is a compile-time constant and the body is one
     // straight-line sequence (exact wait counts).
@@ -330,25 +344,25 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       for (int j = 0; j < kGemmUnroll; ++j) {
         const uint32_t s = s0 + j;
         const int cj = 1 + j;  // s modulo 16
-        dma_x(s + 1);
+        dma_x(s + 2);
         Codes& cc = ((cj >> 3) & 1) ? c1 : c0;        // block of stage s
         Codes& cn = (((cj + 1) >> 3) & 1) ? c1 : c0;  // block of stage s + 1
         Tables& tc = (cj & 1) ? t1 : t0;
         Tables& tn = (cj & 1) ? t0 : t1;
         uint32_t gn, sn, gc, sc;
-        aux_of(cn, (cj + 1) & 7, gn, sn);
-        read_tables(gn, sn, tn);
         aux_of(cc, cj & 7, gc, sc);
         write_w((uint32_t)(cj & 1), sc, cc.d, tc);
+        aux_of(cn, (cj + 1) & 7, gn, sn);
+        read_tables(gn, sn, tn);
         if ((cj & 7) == 7) load_codes((s >> 3) + 2, cc);
-        // in flight after the DMA of stage s: code loads of step s - 1, the
-        // DMA of stage s + 1, code loads of step s (5 loads per code set; at
-        // most one of the two steps loads codes).  cj is a constant once the
-        // loop is unrolled, so one branch remains.
-        if (((cj - 1) & 7) == 7 || (cj & 7) == 7)
-          stage_barrier<L::kDma + 5>();
+        // in flight after the DMA of stage s: code loads of steps s - 2 and
+        // s - 1, the DMA of stages s + 1 and s + 2, code loads of step s (5
+        // loads per code set; at most one of the three steps loads codes).
+        // cj is a constant once the loop is unrolled, so one branch remains.
+        if (((cj - 2) & 7) == 7 || ((cj - 1) & 7) == 7 || (cj & 7) == 7)
+          stage_barrier<2 * L::kDma + 5, 4>();
         else
-          stage_barrier<L::kDma>();
+          stage_barrier<2 * L::kDma, 4>();
       }
     }
     return;
@@ -371,7 +385,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   struct Frags {
     u32x4 a[4], b[NT];
   };
-  // fragments of stage s: activation tile abuf (s % 3), weight tile s & 1
+  // fragments of stage s: activation tile abuf (s & 3), weight tile s & 1
   auto read_frags = [&](uint32_t abuf, uint32_t s, Frags& F) {
     const uint32_t abase = aofs + abuf * L::kAStage;
 #pragma unroll
@@ -407,7 +421,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       }
   };
 
-  auto next3 = [](uint32_t b) { return b == 2 ? 0u : b + 1; };
+  auto next_tile = [](uint32_t b) { return (b + 1) & 3u; };
   // Rows 0-1 of stage F, one MFMA after another.
   auto mfma_rows01 = [&](const Frags& F) {
 #pragma unroll
@@ -431,11 +445,11 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   for (; s + 2 < a.nk; s += 2) {
     mfma_rows01(f0);
     stage_barrier<0>();
-    ab = next3(ab);
+    ab = next_tile(ab);
     mfma_rows_reading(f0, ab, s + 1, f1);
     mfma_rows01(f1);
     stage_barrier<0>();
-    ab = next3(ab);
+    ab = next_tile(ab);
     mfma_rows_reading(f1, ab, s + 2, f0);
   }
   // the last one or two stages
@@ -443,7 +457,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   mfma_rows(f0, 2);
   if (s + 1 < a.nk) {
     __syncthreads();
-    read_frags(next3(ab), s + 1, f1);
+    read_frags(next_tile(ab), s + 1, f1);
     mfma_rows(f1, 0);
     mfma_rows(f1, 2);
   }
