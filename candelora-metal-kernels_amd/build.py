@@ -46,6 +46,7 @@ HIP_SOURCES = [
     "iq2xxs_gemv.hip",
     "iq2xxs_gemm.hip",
     "iq2xxs_simple.hip",
+    "iq_variants.hip",
     "cmk_iq2.cpp",
 ]
 

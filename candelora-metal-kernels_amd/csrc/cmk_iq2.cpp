@@ -39,15 +39,9 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(CMK_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 
-const char* variant_name(int v) {
-  switch (v) {
-    case CMK_IQ2_XXS: return "Iq2Xxs";
-    case CMK_IQ2_XS: return "Iq2Xs";
-    case CMK_IQ2_S: return "Iq2S";
-    case CMK_IQ3_S: return "Iq3S";
-    default: return "Unknown";
-  }
-}
+// bytes_per_block / scales_per_block (src/iq2_matmul.rs:13-29,39-57).
+size_t bytes_per_block(int v) { return v == CMK_IQ2_XXS ? 64 : cmk::variant_bytes_per_block(v); }
+size_t scales_per_block(int v) { return v == CMK_IQ2_XXS ? 2 : cmk::variant_scales_per_block(v); }
 
 // Largest m served by the GEMV family when x is f16/bf16 (above it: MFMA GEMM).
 constexpr size_t kGemvMaxM = 16;
@@ -84,7 +78,7 @@ int current_cu_count(int* cus) {
 }
 
 // Path decision shared by the launch, the workspace query and the path query.
-enum class Path { Gemv, Gemm, Simple };
+enum class Path { Gemv, Gemm, Simple, Variant };
 
 // Null pointers stand for allocator-aligned buffers (queries made before the
 // buffers exist).
@@ -107,7 +101,7 @@ size_t row_scale_bytes(size_t m) {
 }
 
 size_t workspace_for(Path p, bool w8a8, size_t m, uint32_t in_dim) {
-  if (!w8a8 || p == Path::Gemv) return 0;
+  if (!w8a8 || p == Path::Gemv) return 0;  // Simple and Variant: row scales only
   if (p == Path::Gemm) return row_scale_bytes(m) + cmk::gemm_w8a8_scratch_bytes((uint32_t)m, in_dim);
   return row_scale_bytes(m);
 }
@@ -129,13 +123,8 @@ int validate_matmul(int x_dtype, size_t m, size_t out_dim, size_t in_dim, int va
   // iq2_matmul_metal guards (src/iq2_matmul.rs:210-311)
   if (out_dim == 0 || in_dim == 0)
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul expects non-zero dimensions");
-  if (variant != CMK_IQ2_XXS) {
-    if (variant < CMK_IQ2_XXS || variant > CMK_IQ3_S)
-      return fail(CMK_ERR_INVALID_ARGUMENT, "invalid iq2 variant: %d", variant);
-    return fail(CMK_ERR_UNSUPPORTED,
-                "iq2_matmul variant %s is not implemented by the ROCm backend (Iq2Xxs only)",
-                variant_name(variant));
-  }
+  if (variant < CMK_IQ2_XXS || variant > CMK_IQ3_S)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "invalid iq2 variant: %d", variant);
   if (x_dtype != CMK_F32 && x_dtype != CMK_F16 && x_dtype != CMK_BF16)
     return fail(CMK_ERR_INVALID_ARGUMENT,
                 *mode == CMK_ACT_QUANT_W8A8 ? "iq2_matmul_w8a8 unsupported x dtype: %d"
@@ -143,9 +132,10 @@ int validate_matmul(int x_dtype, size_t m, size_t out_dim, size_t in_dim, int va
                 x_dtype);
   const size_t bpr = (in_dim + 255) / 256;
   size_t blocks, expected_bytes, expected_scales;
-  if (!checked_mul(out_dim, bpr, &blocks) || !checked_mul(blocks, 64, &expected_bytes))
+  if (!checked_mul(out_dim, bpr, &blocks) ||
+      !checked_mul(blocks, bytes_per_block(variant), &expected_bytes))
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul bytes size overflow");
-  if (!checked_mul(blocks, 2, &expected_scales))
+  if (!checked_mul(blocks, scales_per_block(variant), &expected_scales))
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul scales size overflow");
   if (check_sizes) {
     if (wb_len < expected_bytes)
@@ -191,7 +181,9 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
                            &dims);
   if (rc != CMK_OK) return rc;
   // Assume allocator-aligned buffers (hipMalloc gives 256-byte alignment).
-  Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, nullptr, nullptr, nullptr);
+  Path p = variant != CMK_IQ2_XXS
+               ? Path::Variant
+               : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, nullptr, nullptr, nullptr);
   // The simple path can still be chosen at launch for unaligned weights; report
   // the larger need so either choice is covered.
   size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, m, dims.in_dim);
@@ -236,7 +228,9 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_matmul out must be 4-byte aligned");
 
   const bool w8a8 = md == CMK_ACT_QUANT_W8A8;
-  Path p = choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x, weight_bytes, weight_scales);
+  Path p = variant != CMK_IQ2_XXS ? Path::Variant
+                                  : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x,
+                                                weight_bytes, weight_scales);
   const size_t need_ws = workspace_for(p, w8a8, m, dims.in_dim);
   if (need_ws > 0 && (workspace == nullptr || workspace_bytes < need_ws))
     return fail(CMK_ERR_INVALID_ARGUMENT,
@@ -271,6 +265,11 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
       e = cmk::launch_iq2xxs_matmul_simple(x, (int)x_dtype, dims.m, weight_bytes, weight_scales,
                                            out, dims.out_dim, dims.in_dim, row_inv, cus, s);
       break;
+    case Path::Variant:
+      e = cmk::launch_iq_variant_matmul((int)variant, x, (int)x_dtype, dims.m, weight_bytes,
+                                        weight_scales, out, dims.out_dim, dims.in_dim, row_inv,
+                                        cus, s);
+      break;
   }
   if (e != hipSuccess) return hip_fail(e, "iq2_matmul launch");
   return ok();
@@ -283,22 +282,17 @@ int cmk_iq2_dequantize(const uint8_t* weight_bytes, size_t weight_bytes_len,
   // iq2_dequantize_to_f16_metal guards (src/iq2_matmul.rs:367-433)
   if (out_dim == 0 || in_dim == 0)
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 expects non-zero dimensions");
-  if (variant != CMK_IQ2_XXS) {
-    if ((int)variant < CMK_IQ2_XXS || (int)variant > CMK_IQ3_S)
-      return fail(CMK_ERR_INVALID_ARGUMENT, "invalid iq2 variant: %d", (int)variant);
-    return fail(CMK_ERR_UNSUPPORTED,
-                "iq2_dequantize_to_f16 variant %s is not implemented by the ROCm backend "
-                "(Iq2Xxs only)",
-                variant_name((int)variant));
-  }
+  if ((int)variant < CMK_IQ2_XXS || (int)variant > CMK_IQ3_S)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "invalid iq2 variant: %d", (int)variant);
   if (out_dtype != CMK_F32 && out_dtype != CMK_F16 && out_dtype != CMK_BF16)
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize unsupported output dtype: %d",
                 (int)out_dtype);
   const size_t bpr = (in_dim + 255) / 256;
   size_t blocks, expected_bytes, expected_scales, total;
-  if (!checked_mul(out_dim, bpr, &blocks) || !checked_mul(blocks, 64, &expected_bytes))
+  if (!checked_mul(out_dim, bpr, &blocks) ||
+      !checked_mul(blocks, bytes_per_block((int)variant), &expected_bytes))
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 bytes size overflow");
-  if (!checked_mul(blocks, 2, &expected_scales))
+  if (!checked_mul(blocks, scales_per_block((int)variant), &expected_scales))
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 scales size overflow");
   if (weight_bytes_len < expected_bytes)
     return fail(CMK_ERR_INVALID_ARGUMENT,
@@ -314,7 +308,7 @@ int cmk_iq2_dequantize(const uint8_t* weight_bytes, size_t weight_bytes_len,
   if (in_dim > UINT32_MAX) return fail(CMK_ERR_INVALID_ARGUMENT, "in_dim too large");
   if (!weight_bytes || !weight_scales || !out)
     return fail(CMK_ERR_INVALID_ARGUMENT, "iq2_dequantize_to_f16 null pointer argument");
-  if (!aligned(weight_bytes, 8) || !aligned(weight_scales, 2))
+  if (variant == CMK_IQ2_XXS && (!aligned(weight_bytes, 8) || !aligned(weight_scales, 2)))
     return fail(CMK_ERR_INVALID_ARGUMENT,
                 "iq2_dequantize_to_f16 needs 8-byte aligned weight_bytes and 2-byte aligned "
                 "weight_scales");
@@ -323,9 +317,14 @@ int cmk_iq2_dequantize(const uint8_t* weight_bytes, size_t weight_bytes_len,
   int cus = 0;
   int rc = current_cu_count(&cus);
   if (rc != CMK_OK) return rc;
-  hipError_t e = cmk::launch_iq2xxs_dequant(weight_bytes, weight_scales, out, (int)out_dtype,
-                                            (uint32_t)out_dim, (uint32_t)in_dim, cus,
-                                            static_cast<hipStream_t>(stream));
+  hipError_t e =
+      variant == CMK_IQ2_XXS
+          ? cmk::launch_iq2xxs_dequant(weight_bytes, weight_scales, out, (int)out_dtype,
+                                       (uint32_t)out_dim, (uint32_t)in_dim, cus,
+                                       static_cast<hipStream_t>(stream))
+          : cmk::launch_iq_variant_dequant((int)variant, weight_bytes, weight_scales, out,
+                                           (int)out_dtype, (uint32_t)out_dim, (uint32_t)in_dim,
+                                           cus, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "iq2_dequantize launch");
   return ok();
 }

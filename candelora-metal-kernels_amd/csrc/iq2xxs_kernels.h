@@ -46,4 +46,17 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               const float* row_inv, void* xq, hipStream_t stream);
 
+// IQ2_XS (1), IQ2_S (2), IQ3_S (3): bytes / scales per 256-weight block
+// (0 for any other variant), and the portable matmul (any m, any alignment;
+// row_inv as for the simple path) and dequantisation of those formats.
+size_t variant_bytes_per_block(int variant);
+size_t variant_scales_per_block(int variant);
+hipError_t launch_iq_variant_matmul(int variant, const void* x, int x_dtype, uint32_t m,
+                                    const uint8_t* wb, const uint8_t* ws, float* out,
+                                    uint32_t out_dim, uint32_t in_dim, const float* row_inv,
+                                    int num_cus, hipStream_t stream);
+hipError_t launch_iq_variant_dequant(int variant, const uint8_t* wb, const uint8_t* ws, void* out,
+                                     int out_kind, uint32_t out_dim, uint32_t in_dim, int num_cus,
+                                     hipStream_t stream);
+
 }  // namespace cmk

@@ -49,8 +49,10 @@ typedef enum cmk_status {
  * reference accepts for x: F32, F16, BF16 (src/iq2_matmul.rs:59-75). */
 typedef enum cmk_dtype { CMK_F32 = 0, CMK_F16 = 1, CMK_BF16 = 2 } cmk_dtype;
 
-/* Iq2MatmulVariant (src/iq2_matmul.rs:31-37).  Only IQ2_XXS is implemented;
- * the others return CMK_ERR_UNSUPPORTED. */
+/* Iq2MatmulVariant (src/iq2_matmul.rs:31-37).  All four are implemented: IQ2_XXS
+ * on the tuned GEMV / GEMM kernels, IQ2_XS / IQ2_S / IQ3_S on a portable wave-per-
+ * row kernel (any m, any buffer alignment).  Bytes / scales per 256-weight block:
+ * 64/2, 64/10, 72/10, 104/6 (src/iq2_matmul.rs:13-29). */
 typedef enum cmk_iq2_variant {
     CMK_IQ2_XXS = 0,
     CMK_IQ2_XS = 1,
@@ -107,11 +109,14 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
 /*
  * out[out_dim, in_dim] = dequantised W in out_dtype (F16, BF16 or F32).
  * Replaces iq2_dequantize_to_f16_metal (src/iq2_matmul.rs:367-505) reached
- * from iq2_dequantize_to_f16 (:594-602), whose kernel is
- * iq2_xxs_dequantize_f16 (iq2_matmul.metal:868-887).  Every value is the
- * single round-to-nearest-even of the exact product d*(0.5+s)*0.25*g*sign;
+ * from iq2_dequantize_to_f16 (:594-602), whose kernels are the four
+ * *_dequantize_f16 kernels (iq2_matmul.metal:868-950, decodes :701-866).
+ * Every value is the single round-to-nearest-even of the exact product
+ * dl*g*sign (dl = d*(0.5+s)*0.25 for the IQ2 formats, d*(1+2s) for IQ3_S);
  * F32 output is that exact product.  F16 is the reference's output type;
- * BF16/F32 are this build's extensions on the same boundary.
+ * BF16/F32 are this build's extensions on the same boundary.  IQ2_XXS needs
+ * 8-byte aligned weight_bytes and 2-byte aligned weight_scales; the other
+ * variants take any alignment.
  */
 int cmk_iq2_dequantize(const uint8_t *weight_bytes, size_t weight_bytes_len,
                        const uint8_t *weight_scales, size_t weight_scales_len,

@@ -55,6 +55,19 @@ def lib():
         L.oracle_iq2xxs_dequantize_f16.argtypes = [P, P, S, S, P]
         L.oracle_iq2xxs_dequantize_bf16.argtypes = [P, P, S, S, P]
         L.oracle_iq2xxs_matmul_f64.argtypes = [P, S, S, S, P, P, P, P]
+        I = ctypes.c_int
+        L.oracle_iq_bytes_per_block.argtypes = [I]
+        L.oracle_iq_bytes_per_block.restype = S
+        L.oracle_iq_scales_per_block.argtypes = [I]
+        L.oracle_iq_scales_per_block.restype = S
+        L.oracle_iq_grid.argtypes = [I, P]
+        L.oracle_iq_grid.restype = S
+        L.oracle_iq_matmul_reference.argtypes = [I, P, S, S, S, P, P, P]
+        L.oracle_iq_matmul_reference_w8a8.argtypes = [I, P, S, S, S, P, P, P]
+        L.oracle_iq_dequantize_f32.argtypes = [I, P, P, S, S, P]
+        L.oracle_iq_dequantize_f16.argtypes = [I, P, P, S, S, P]
+        L.oracle_iq_dequantize_bf16.argtypes = [I, P, P, S, S, P]
+        L.oracle_iq_matmul_f64.argtypes = [I, P, S, S, S, P, P, P, P]
         _lib = L
     return _lib
 
@@ -170,6 +183,74 @@ def matmul_f64(x, m, out_dim, in_dim, wb, ws):
     out = np.zeros((m, out_dim), np.float64)
     sc = np.zeros((m, out_dim), np.float64)
     lib().oracle_iq2xxs_matmul_f64(_p(x), m, out_dim, in_dim, _p(wb), _p(ws), _p(out), _p(sc))
+    return out, sc
+
+
+# ---- all four variants (iq_variants_oracle.c; variant 0 = IQ2_XXS) ----------
+
+IQ2_XXS, IQ2_XS, IQ2_S, IQ3_S = 0, 1, 2, 3
+
+
+def bytes_per_block(variant: int) -> int:
+    return lib().oracle_iq_bytes_per_block(variant)
+
+
+def scales_per_block(variant: int) -> int:
+    return lib().oracle_iq_scales_per_block(variant)
+
+
+def grid(variant: int) -> np.ndarray:
+    """The variant's decoded codebook (u64 values; IQ3_S entries are u32)."""
+    n = lib().oracle_iq_grid(variant, None)
+    out = np.zeros(n, np.uint64)
+    lib().oracle_iq_grid(variant, _p(out))
+    return out
+
+
+def variant_matmul_reference(variant, x, m, out_dim, in_dim, wb, ws) -> np.ndarray:
+    x = _f32(x)
+    wb, ws = _u8(wb), _u8(ws)
+    out = np.zeros((m, out_dim), np.float32)
+    lib().oracle_iq_matmul_reference(variant, _p(x), m, out_dim, in_dim, _p(wb), _p(ws), _p(out))
+    return out
+
+
+def variant_matmul_reference_w8a8(variant, x, m, out_dim, in_dim, wb, ws) -> np.ndarray:
+    x = _f32(x)
+    wb, ws = _u8(wb), _u8(ws)
+    out = np.zeros((m, out_dim), np.float32)
+    lib().oracle_iq_matmul_reference_w8a8(variant, _p(x), m, out_dim, in_dim, _p(wb), _p(ws),
+                                          _p(out))
+    return out
+
+
+def variant_dequantize_f32(variant, wb, ws, out_dim, in_dim) -> np.ndarray:
+    wb, ws = _u8(wb), _u8(ws)
+    out = np.zeros((out_dim, in_dim), np.float32)
+    lib().oracle_iq_dequantize_f32(variant, _p(wb), _p(ws), out_dim, in_dim, _p(out))
+    return out
+
+
+def variant_dequantize_f16_bits(variant, wb, ws, out_dim, in_dim) -> np.ndarray:
+    wb, ws = _u8(wb), _u8(ws)
+    out = np.zeros((out_dim, in_dim), np.uint16)
+    lib().oracle_iq_dequantize_f16(variant, _p(wb), _p(ws), out_dim, in_dim, _p(out))
+    return out
+
+
+def variant_dequantize_bf16_bits(variant, wb, ws, out_dim, in_dim) -> np.ndarray:
+    wb, ws = _u8(wb), _u8(ws)
+    out = np.zeros((out_dim, in_dim), np.uint16)
+    lib().oracle_iq_dequantize_bf16(variant, _p(wb), _p(ws), out_dim, in_dim, _p(out))
+    return out
+
+
+def variant_matmul_f64(variant, x, m, out_dim, in_dim, wb, ws):
+    x = _f32(x)
+    wb, ws = _u8(wb), _u8(ws)
+    out = np.zeros((m, out_dim), np.float64)
+    sc = np.zeros((m, out_dim), np.float64)
+    lib().oracle_iq_matmul_f64(variant, _p(x), m, out_dim, in_dim, _p(wb), _p(ws), _p(out), _p(sc))
     return out, sc
 
 

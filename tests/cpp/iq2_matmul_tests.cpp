@@ -15,6 +15,7 @@
 
 #include "candelora/iq2_matmul.hpp"
 #include "iq2xxs_oracle.h"
+#include "iq_variants_oracle.h"
 
 using namespace candelora;
 
@@ -46,23 +47,37 @@ struct Case {
   size_t m, out_dim, in_dim;
 };
 
-// Inputs of parity_case / w8a8_smoke_case (src/iq2_matmul.rs:1071-1086, 1136-1146).
-Case reference_case(size_t m, size_t out_dim, size_t in_dim, uint32_t bseed, uint32_t sseed,
-                    uint8_t tail) {
+int oracle_variant(Iq2MatmulVariant v) {
+  switch (v) {
+    case Iq2MatmulVariant::Iq2Xxs: return ORACLE_IQ2_XXS;
+    case Iq2MatmulVariant::Iq2Xs: return ORACLE_IQ2_XS;
+    case Iq2MatmulVariant::Iq2S: return ORACLE_IQ2_S;
+    default: return ORACLE_IQ3_S;
+  }
+}
+
+// Inputs of parity_case / w8a8_smoke_case (src/iq2_matmul.rs:1071-1086, 1136-1146),
+// sized by the variant's bytes / scales per block.
+Case reference_case(Iq2MatmulVariant variant, size_t m, size_t out_dim, size_t in_dim,
+                    uint32_t bseed, uint32_t sseed, uint8_t tail) {
   Case c{{}, {}, {}, m, out_dim, in_dim};
   const size_t bpr = (in_dim + 255) / 256, nb = out_dim * bpr;
-  c.wb.resize(nb * 64);
-  c.ws.resize(nb * 2);
+  const int ov = oracle_variant(variant);
+  const size_t spb = oracle_iq_scales_per_block(ov);
+  c.wb.resize(nb * oracle_iq_bytes_per_block(ov));
+  c.ws.resize(nb * spb);
   oracle_lcg_fill(c.wb.data(), c.wb.size(), bseed);
   oracle_lcg_fill(c.ws.data(), c.ws.size(), sseed);
-  oracle_force_f16_one_per_block(c.ws.data(), c.ws.size(), 2);
+  oracle_force_f16_one_per_block(c.ws.data(), c.ws.size(), spb);
   if (!c.wb.empty()) c.wb.back() = tail;
   c.x.resize(m * in_dim);
   oracle_deterministic_x(c.x.data(), c.x.size());
   return c;
 }
 
-Case parity_inputs() { return reference_case(2, 7, 320, 0xA11CE5ED, 0xC0FFEE12, 0x5A); }
+Case parity_inputs(Iq2MatmulVariant v = Iq2MatmulVariant::Iq2Xxs) {
+  return reference_case(v, 2, 7, 320, 0xA11CE5ED, 0xC0FFEE12, 0x5A);
+}
 
 struct DevCase {
   Tensor x, wb, ws;
@@ -116,13 +131,13 @@ void errors_before_any_device_access() {
 // ------------------------------------------------------------------ GPU tests
 
 void parity_case(Iq2MatmulVariant variant) {
-  Case c = parity_inputs();
+  Case c = parity_inputs(variant);
   DevCase d = upload(c, Device::hip(0));
   Tensor y = iq2_matmul(d.x, d.wb, d.ws, 7, 320, variant);
   synchronize();
   std::vector<float> ref(c.m * c.out_dim);
-  oracle_iq2xxs_matmul_reference(c.x.data(), c.m, c.out_dim, c.in_dim, c.wb.data(), c.ws.data(),
-                                 ref.data());
+  oracle_iq_matmul_reference(oracle_variant(variant), c.x.data(), c.m, c.out_dim, c.in_dim,
+                             c.wb.data(), c.ws.data(), ref.data());
   CHECK(y.dims() == (std::vector<size_t>{2, 7}), "output shape");
   CHECK(y.dtype() == DType::F32, "output dtype");
   const double md = max_abs_diff(y.to_vec<float>(), ref);
@@ -130,19 +145,19 @@ void parity_case(Iq2MatmulVariant variant) {
 }
 
 void parity_case_w8a8(Iq2MatmulVariant variant) {
-  Case c = parity_inputs();
+  Case c = parity_inputs(variant);
   DevCase d = upload(c, Device::hip(0));
   Tensor y = iq2_matmul_with_activation_quant(d.x, d.wb, d.ws, 7, 320, variant,
                                               {ActivationQuantMode::W8A8, false});
   std::vector<float> ref(c.m * c.out_dim);
-  oracle_iq2xxs_matmul_reference_w8a8(c.x.data(), c.m, c.out_dim, c.in_dim, c.wb.data(),
-                                      c.ws.data(), ref.data());
+  oracle_iq_matmul_reference_w8a8(oracle_variant(variant), c.x.data(), c.m, c.out_dim, c.in_dim,
+                                  c.wb.data(), c.ws.data(), ref.data());
   const double md = max_abs_diff(y.to_vec<float>(), ref);
   CHECK(md <= 3e-3, "IQ2 W8A8 parity max_abs too high: " + std::to_string(md));  // :1239,1247
 }
 
 void w8a8_smoke_case(Iq2MatmulVariant variant) {
-  Case c = reference_case(2, 6, 320, 0x0BADC0DE, 0xD15EA5ED, 0xC3);
+  Case c = reference_case(variant, 2, 6, 320, 0x0BADC0DE, 0xD15EA5ED, 0xC3);
   DevCase d = upload(c, Device::hip(0));
   Tensor y = iq2_matmul_with_activation_quant(d.x, d.wb, d.ws, 6, 320, variant,
                                               {ActivationQuantMode::W8A8, false});
@@ -150,22 +165,19 @@ void w8a8_smoke_case(Iq2MatmulVariant variant) {
   for (float v : y.to_vec<float>()) CHECK(std::isfinite(v), "non-finite output");
 }
 
+// src/iq2_matmul.rs:1255-1313, one test per variant and case.
 void cpu_vs_hip_parity_iq2_xxs() { parity_case(Iq2MatmulVariant::Iq2Xxs); }
+void cpu_vs_hip_parity_iq2_xs() { parity_case(Iq2MatmulVariant::Iq2Xs); }
+void cpu_vs_hip_parity_iq2_s() { parity_case(Iq2MatmulVariant::Iq2S); }
+void cpu_vs_hip_parity_iq3_s() { parity_case(Iq2MatmulVariant::Iq3S); }
 void cpu_vs_hip_parity_w8a8_iq2_xxs() { parity_case_w8a8(Iq2MatmulVariant::Iq2Xxs); }
+void cpu_vs_hip_parity_w8a8_iq2_xs() { parity_case_w8a8(Iq2MatmulVariant::Iq2Xs); }
+void cpu_vs_hip_parity_w8a8_iq2_s() { parity_case_w8a8(Iq2MatmulVariant::Iq2S); }
+void cpu_vs_hip_parity_w8a8_iq3_s() { parity_case_w8a8(Iq2MatmulVariant::Iq3S); }
 void w8a8_kernel_smoke_iq2_xxs() { w8a8_smoke_case(Iq2MatmulVariant::Iq2Xxs); }
-
-// The other codebooks are outside this build: the ops fail with a clear error.
-void other_variants_report_not_implemented() {
-  Case c = parity_inputs();
-  DevCase d = upload(c, Device::hip(0));
-  std::vector<uint8_t> big(7 * 2 * 104 + 64, 0), bigs(7 * 2 * 10, 0);
-  Tensor wb = Tensor::from_vec(big, {big.size()}, DType::U8, Device::hip(0));
-  Tensor ws = Tensor::from_vec(bigs, {bigs.size()}, DType::U8, Device::hip(0));
-  for (auto v : {Iq2MatmulVariant::Iq2Xs, Iq2MatmulVariant::Iq2S, Iq2MatmulVariant::Iq3S}) {
-    std::string e = expect_error([&] { iq2_matmul(d.x, wb, ws, 7, 320, v); });
-    CHECK(e.find("not implemented by the ROCm backend") != std::string::npos, e);
-  }
-}
+void w8a8_kernel_smoke_iq2_xs() { w8a8_smoke_case(Iq2MatmulVariant::Iq2Xs); }
+void w8a8_kernel_smoke_iq2_s() { w8a8_smoke_case(Iq2MatmulVariant::Iq2S); }
+void w8a8_kernel_smoke_iq3_s() { w8a8_smoke_case(Iq2MatmulVariant::Iq3S); }
 
 void dequantize_to_f16_bit_exact_iq2_xxs() {
   Case c = parity_inputs();
@@ -248,9 +260,17 @@ const Test kTests[] = {
     {"activation_quant_config_contract", false, activation_quant_config_contract},
     {"errors_before_any_device_access", false, errors_before_any_device_access},
     {"cpu_vs_hip_parity_iq2_xxs", true, cpu_vs_hip_parity_iq2_xxs},
+    {"cpu_vs_hip_parity_iq2_xs", true, cpu_vs_hip_parity_iq2_xs},
+    {"cpu_vs_hip_parity_iq2_s", true, cpu_vs_hip_parity_iq2_s},
+    {"cpu_vs_hip_parity_iq3_s", true, cpu_vs_hip_parity_iq3_s},
     {"cpu_vs_hip_parity_w8a8_iq2_xxs", true, cpu_vs_hip_parity_w8a8_iq2_xxs},
+    {"cpu_vs_hip_parity_w8a8_iq2_xs", true, cpu_vs_hip_parity_w8a8_iq2_xs},
+    {"cpu_vs_hip_parity_w8a8_iq2_s", true, cpu_vs_hip_parity_w8a8_iq2_s},
+    {"cpu_vs_hip_parity_w8a8_iq3_s", true, cpu_vs_hip_parity_w8a8_iq3_s},
     {"w8a8_kernel_smoke_iq2_xxs", true, w8a8_kernel_smoke_iq2_xxs},
-    {"other_variants_report_not_implemented", true, other_variants_report_not_implemented},
+    {"w8a8_kernel_smoke_iq2_xs", true, w8a8_kernel_smoke_iq2_xs},
+    {"w8a8_kernel_smoke_iq2_s", true, w8a8_kernel_smoke_iq2_s},
+    {"w8a8_kernel_smoke_iq3_s", true, w8a8_kernel_smoke_iq3_s},
     {"dequantize_to_f16_bit_exact_iq2_xxs", true, dequantize_to_f16_bit_exact_iq2_xxs},
     {"argument_errors_on_device", true, argument_errors_on_device},
     {"layouts_rank1_strided_and_offset_inputs", true, layouts_rank1_strided_and_offset_inputs},

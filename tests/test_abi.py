@@ -62,12 +62,26 @@ def test_w4a8_strict_and_fallback(cabi):
     assert msg == "iq2_matmul expects non-zero dimensions"
 
 
-def test_other_variants_unsupported(cabi):
-    for v, name in ((1, "Iq2Xs"), (2, "Iq2S"), (3, "Iq3S")):
-        rc, msg = call(cabi, variant=v)
-        assert rc == cabi.CMK_ERR_UNSUPPORTED and name in msg
+# bytes / scales per block of each variant (src/iq2_matmul.rs:13-29,39-57)
+VARIANT_SIZES = {0: (64, 2), 1: (64, 10), 2: (72, 10), 3: (104, 6)}
+
+
+def test_variant_size_checks(cabi):
+    """Every variant is served; its buffers are checked against its own block
+    sizes with the reference's texts (src/iq2_matmul.rs:238-259)."""
+    for v, (bpb, spb) in VARIANT_SIZES.items():
+        need_b, need_s = 7 * 2 * bpb, 7 * 2 * spb
+        rc, msg = call(cabi, variant=v, wb_len=need_b - 1)
+        assert rc == cabi.CMK_ERR_INVALID_ARGUMENT
+        assert msg == f"iq2_matmul weight_bytes too small: got {need_b - 1} expected at least {need_b}"
+        rc, msg = call(cabi, variant=v, wb_len=need_b, ws_len=need_s - 1)
+        assert msg == (f"iq2_matmul weight_scales too small: got {need_s - 1} expected at least "
+                       f"{need_s}")
+        # exact sizes pass the size checks and stop at the missing x buffer
+        rc, msg = call(cabi, variant=v, wb_len=need_b, ws_len=need_s)
+        assert msg == "iq2_matmul x too small: got 0 expected at least 320"
     rc, msg = call(cabi, variant=9)
-    assert rc == cabi.CMK_ERR_INVALID_ARGUMENT
+    assert rc == cabi.CMK_ERR_INVALID_ARGUMENT and msg == "invalid iq2 variant: 9"
 
 
 def test_bad_dtype(cabi):
@@ -119,7 +133,12 @@ def test_dequantize_validation(cabi):
                              "least 896")
     assert dq(wsl=1)[1] == ("iq2_dequantize_to_f16 weight_scales too small: got 1 expected at "
                             "least 28")
-    assert dq(v=2)[0] == cabi.CMK_ERR_UNSUPPORTED
+    # IQ2_S: 72 + 10 bytes per block
+    assert dq(v=2)[1] == ("iq2_dequantize_to_f16 weight_bytes too small: got 896 expected at "
+                          "least 1008")
+    assert dq(v=2, wbl=1008)[1] == ("iq2_dequantize_to_f16 weight_scales too small: got 28 "
+                                    "expected at least 140")
+    assert dq(v=3, wbl=1456, wsl=84)[1] == "iq2_dequantize_to_f16 null pointer argument"
     assert "unsupported output dtype" in dq(dt=5)[1]
     assert dq()[1] == "iq2_dequantize_to_f16 null pointer argument"
 

@@ -1,0 +1,155 @@
+"""GPU parity of the IQ2_XS / IQ2_S / IQ3_S path against the CPU oracle.
+
+Bars (as for IQ2_XXS):
+  * dequantisation: bit-exact (f16, bf16, f32) against the oracle, for aligned
+    and unaligned weight buffers;
+  * the reference's in-test cases for every variant (src/iq2_matmul.rs:
+    1065-1253, 1255-1313): |gpu - oracle| <= 2e-3 (mode Off), <= 3e-3 (W8A8);
+  * matmul at other shapes, against the fp64-accumulated oracle:
+      cond = max_i |y_i - y64_i| / sum_k |x_k w_ik|   (<= 1e-5)
+      rel  = max over outputs with |y64_i| >= 1e-2 max|y64| of |y_i - y64_i|/|y64_i|
+             (<= 1e-3, the GEMV bar).
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+XS, S, S3 = 1, 2, 3
+VARIANTS = [XS, S, S3]
+
+
+@pytest.fixture(scope="module")
+def dev(pkg):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    pkg.cabi.lib()  # fail loudly when the HIP library is missing
+    return torch.device("cuda:0")
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def variant_enum(pkg, v):
+    return pkg.Iq2MatmulVariant(v)
+
+
+def reference_case(oracle, v, m=2, out_dim=7, in_dim=320, bseed=0xA11CE5ED, sseed=0xC0FFEE12,
+                   tail=0x5A):
+    """parity_case / w8a8_smoke_case inputs (src/iq2_matmul.rs:1071-1086,1136-1146)
+    sized by the variant's bytes / scales per block."""
+    bpr = -(-in_dim // 256)
+    nb = out_dim * bpr
+    spb = oracle.scales_per_block(v)
+    wb = oracle.lcg_fill(nb * oracle.bytes_per_block(v), bseed)
+    ws = oracle.force_f16_one_per_block(oracle.lcg_fill(nb * spb, sseed), spb)
+    wb[-1] = tail
+    x = oracle.deterministic_x(m * in_dim).reshape(m, in_dim)
+    return x, wb, ws
+
+
+def random_weights(oracle, v, out_dim, in_dim, seed):
+    rng = np.random.default_rng(seed)
+    nb = out_dim * (-(-in_dim // 256))
+    bpb, spb = oracle.bytes_per_block(v), oracle.scales_per_block(v)
+    wb = rng.integers(0, 256, nb * bpb, dtype=np.uint8)
+    ws = rng.integers(0, 256, nb * spb, dtype=np.uint8)
+    ws[1::spb] = rng.integers(0x10, 0x20, nb, dtype=np.uint8)  # d ~ 1e-3 .. 1e-2, finite
+    return wb, ws
+
+
+def errors(y, y64, scale):
+    y = np.asarray(y, np.float64)
+    cond = float(np.max(np.abs(y - y64) / np.maximum(scale, 1e-300)))
+    big = np.abs(y64) >= 1e-2 * np.max(np.abs(y64))
+    rel = float(np.max(np.abs(y - y64)[big] / np.abs(y64[big]))) if big.any() else 0.0
+    return cond, rel
+
+
+@pytest.mark.parametrize("v", VARIANTS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_cpu_vs_hip_parity(pkg, oracle, dev, v, dtype):
+    x, wb, ws = reference_case(oracle, v)
+    xt = to_dev(x, dev).to(dtype)
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), 7, 320, variant_enum(pkg, v))
+    torch.cuda.synchronize()
+    ref = oracle.variant_matmul_reference(v, xt.float().cpu().numpy(), 2, 7, 320, wb, ws)
+    diff = np.abs(y.cpu().numpy() - ref)
+    assert diff.max() <= 2e-3, diff.max()  # src/iq2_matmul.rs:1113,1121
+
+
+@pytest.mark.parametrize("v", VARIANTS)
+def test_cpu_vs_hip_parity_w8a8(pkg, oracle, dev, v):
+    x, wb, ws = reference_case(oracle, v)
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), 7,
+                                             320, variant_enum(pkg, v), cfg)
+    ref = oracle.variant_matmul_reference_w8a8(v, x, 2, 7, 320, wb, ws)
+    diff = np.abs(y.cpu().numpy() - ref)
+    assert diff.max() <= 3e-3, diff.max()  # src/iq2_matmul.rs:1239,1247
+
+
+@pytest.mark.parametrize("v", VARIANTS)
+def test_w8a8_kernel_smoke(pkg, oracle, dev, v):
+    x, wb, ws = reference_case(oracle, v, 2, 6, 320, 0x0BADC0DE, 0xD15EA5ED, 0xC3)
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), 6,
+                                             320, variant_enum(pkg, v), cfg)
+    yh = y.cpu().numpy()
+    assert yh.shape == (2, 6) and np.all(np.isfinite(yh))
+
+
+@pytest.mark.parametrize("v", VARIANTS)
+@pytest.mark.parametrize("out_dim,in_dim", [(7, 320), (64, 4096), (5, 41), (3, 300)])
+def test_dequant_bit_exact(pkg, oracle, dev, v, out_dim, in_dim):
+    wb, ws = random_weights(oracle, v, out_dim, in_dim, 100 * v + out_dim + in_dim)
+    wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
+    ve = variant_enum(pkg, v)
+    f16 = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, ve)
+    assert f16.dtype == torch.float16 and tuple(f16.shape) == (out_dim, in_dim)
+    got = f16.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, oracle.variant_dequantize_f16_bits(v, wb, ws, out_dim, in_dim))
+    bf = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, ve, out_dtype=torch.bfloat16)
+    got = bf.cpu().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, oracle.variant_dequantize_bf16_bits(v, wb, ws, out_dim, in_dim))
+    f32 = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, ve, out_dtype=torch.float32)
+    assert np.array_equal(f32.cpu().numpy().view(np.uint32),
+                          oracle.variant_dequantize_f32(v, wb, ws, out_dim, in_dim).view(np.uint32))
+
+
+@pytest.mark.parametrize("v", VARIANTS)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,out_dim,in_dim", [(1, 64, 4096), (3, 33, 1000), (6, 17, 512)])
+def test_matmul_parity(pkg, oracle, dev, v, dtype, m, out_dim, in_dim):
+    wb, ws = random_weights(oracle, v, out_dim, in_dim, 7 * v + m + in_dim)
+    x = np.random.default_rng(v + m).standard_normal((m, in_dim)).astype(np.float32)
+    xt = to_dev(x, dev).to(dtype)
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim, variant_enum(pkg, v))
+    y64, scale = oracle.variant_matmul_f64(v, xt.float().cpu().numpy(), m, out_dim, in_dim, wb, ws)
+    cond, rel = errors(y.cpu().numpy(), y64, scale)
+    assert cond <= 1e-5, cond
+    assert rel <= 1e-3, rel
+
+
+@pytest.mark.parametrize("v", VARIANTS)
+def test_unaligned_weight_buffers(pkg, oracle, dev, v):
+    """Code and scale bytes at odd device addresses give the same results."""
+    out_dim, in_dim, m = 9, 512, 2
+    wb, ws = random_weights(oracle, v, out_dim, in_dim, 900 + v)
+    x = np.random.default_rng(v).standard_normal((m, in_dim)).astype(np.float32)
+    xt = to_dev(x, dev)
+    ve = variant_enum(pkg, v)
+    wbig = torch.zeros(wb.size + 1, dtype=torch.uint8, device=dev)
+    sbig = torch.zeros(ws.size + 1, dtype=torch.uint8, device=dev)
+    wbig[1:] = to_dev(wb, dev)
+    sbig[1:] = to_dev(ws, dev)
+    y_al = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim, ve)
+    y_un = pkg.iq2_matmul(xt, wbig[1:], sbig[1:], out_dim, in_dim, ve)
+    assert torch.equal(y_al, y_un)
+    d_al = pkg.iq2_dequantize_to_f16(to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim, ve)
+    d_un = pkg.iq2_dequantize_to_f16(wbig[1:], sbig[1:], out_dim, in_dim, ve)
+    assert torch.equal(d_al, d_un)
