@@ -37,6 +37,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 REPO = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(REPO, "candelora-metal-kernels_amd")
 
@@ -77,15 +79,16 @@ class Matmul:
     pointers, so the tensors must stay alive as long as the launch (or a graph
     that captured it) can run."""
 
-    def __init__(self, cabi, x, wb, ws, out, m, k, n, x_dtype, stream):
+    def __init__(self, cabi, x, wb, ws, out, m, k, n, x_dtype, stream, variant=0):
         self.tensors = (x, wb, ws, out)
         self.args = (x.data_ptr(), x_dtype, x.numel(), m, wb.data_ptr(), wb.numel(),
                      ws.data_ptr(), ws.numel(), n, k, out.data_ptr())
         self.cabi = cabi
         self.stream = stream
+        self.variant = variant
 
     def __call__(self):
-        self.cabi.matmul_raw(*self.args, stream=self.stream)
+        self.cabi.matmul_raw(*self.args, variant=self.variant, stream=self.stream)
 
 
 def bench_decode(pkg, torch, stream, steps, warmup):
@@ -191,6 +194,55 @@ def bench_prefill(pkg, torch, stream, steps, warmup, m=512, k=4096, n=14336):
             "gbs": alg_bytes(m, k, n, 2) / t / 1e9, "steps": steps}
 
 
+# IQ2_XS, IQ2_S, IQ3_S: (ABI variant, bytes, scales per 256-weight block)
+VARIANTS = [("iq2_xs", 1, 64, 10), ("iq2_s", 2, 72, 10), ("iq3_s", 3, 104, 6)]
+
+
+def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
+    """The other formats' matmul at the config 1 gate shape (M=1, f32 x): one
+    graph replay of `steps` launches over rotated weight copies per format."""
+    cabi, inputs = pkg.cabi, pkg.inputs
+    dev = torch.device("cuda:0")
+    sh = int(stream.cuda_stream)
+    bpr = math.ceil(k / 256)
+    x = torch.from_numpy(inputs.synthetic_x(1, k)).to(dev)
+    out = torch.empty((1, n), dtype=torch.float32, device=dev)
+    res = {}
+    for name, v, bpb, spb in VARIANTS:
+        rng = np.random.default_rng(v)
+        wb = rng.integers(0, 256, n * bpr * bpb, dtype=np.uint8)
+        ws = rng.integers(0, 256, n * bpr * spb, dtype=np.uint8)
+        ws[1::spb] = rng.integers(0x10, 0x20, n * bpr, dtype=np.uint8)  # finite d
+        w_bytes = wb.size + ws.size
+        copies = max(2, math.ceil(2 * MALL_BYTES / w_bytes))
+        wbt, wst = torch.from_numpy(wb).to(dev), torch.from_numpy(ws).to(dev)
+        reps = [(wbt, wst)] + [(wbt.clone(), wst.clone()) for _ in range(copies - 1)]
+        calls = [Matmul(cabi, x, r[0], r[1], out, 1, k, n, cabi.CMK_F32, sh, v) for r in reps]
+        for c in calls:
+            c()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                calls[i % copies]()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, stop = cabi.Event(), cabi.Event()
+        start.record(sh)
+        graph.replay()
+        stop.record(sh)
+        torch.cuda.synchronize()
+        us = start.elapsed_ms(stop) * 1e3 / steps
+        alg = w_bytes + k * 4 + n * 4
+        res[name] = {"k": k, "n": n, "m": 1, "mean_launch_us": us, "alg_bytes_per_launch": alg,
+                     "gbs": alg / (us * 1e-6) / 1e9,
+                     "frac_of_hbm_peak": alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                     "kernel": f"cmk::iq_variant_matmul_kernel<{v}>", "launches": steps}
+        log(f"[bench] {name}: {us:.2f} us per launch, {res[name]['gbs']:.1f} GB/s")
+        del graph, calls, reps
+    return res
+
+
 def cpu_baseline(pkg, seconds):
     """The oracle (scalar restatement of the reference's CPU reference, OpenMP over
     outputs) on the same decode step; repeated until `seconds` of CPU time."""
@@ -242,6 +294,9 @@ def main():
     # sustained rate rather than the ramp (50 launches read about 15 % slower).
     ap.add_argument("--prefill-steps", type=int, default=400)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="skip the IQ2_XS / IQ2_S / IQ3_S lines")
+    ap.add_argument("--variant-steps", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -280,6 +335,8 @@ def main():
         dec = bench_decode(pkg, torch, stream, args.steps, args.warmup)
         prefill = (None if args.no_prefill
                    else bench_prefill(pkg, torch, stream, args.prefill_steps, 5))
+        variants = (None if args.no_variants
+                    else bench_variants(pkg, torch, stream, args.variant_steps))
     torch.cuda.synchronize()
     value = dec["step_bytes"] * args.steps / (dec["ms"] / 1e3) / 1e9
     achieved = dec["per_launch_bytes"] / (dec["mean_launch_us"] * 1e-6) / 1e9
@@ -315,6 +372,8 @@ def main():
     }
     if prefill is not None:
         line["prefill_m512"] = prefill
+    if variants is not None:
+        line["variants_m1"] = variants
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(pkg, args.cpu_seconds)
     else:

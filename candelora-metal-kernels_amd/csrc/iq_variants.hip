@@ -23,8 +23,12 @@
 //                    high bit per entry, signs[72..104) one byte per group;
 //                    scales: d, then nibble ib32 of bytes 2..5.
 //
-// Matmul: one wave per output row, lanes over sub-blocks, exact weights into
-// fp32 FMA for up to four activation rows at a time, wave reduction.
+// Matmul: the workgroup stages up to four activation rows in LDS as fp32
+// (W8A8: after the reference's qdq), padded by 4 floats per 32 so that the
+// lanes' 16-byte reads of their sub-blocks' columns are conflict-free; each
+// wave then takes four weight rows at once, lanes over sub-blocks, exact
+// weights into fp32 FMA, and reduces across the wave.  Shapes whose staged
+// rows do not fit LDS read x from global memory with one row per wave.
 // Dequantisation: one thread per sub-block, each output the single RNE of its
 // exact weight.  Codebooks are expanded from compact codes into LDS at launch.
 // All code and scale bytes are read with byte loads (any alignment).
@@ -80,6 +84,21 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
 }
 
+// Little-endian loads: byte by byte for any alignment, or (kAligned: weight
+// bytes 4-byte and scales 2-byte aligned; every offset used below is then a
+// multiple of the access size) one load each.
+template <bool kAligned>
+struct Ld {
+  static __device__ __forceinline__ uint32_t u16(const uint8_t* p) {
+    if constexpr (kAligned) return *reinterpret_cast<const uint16_t*>(p);
+    return ld_u16(p);
+  }
+  static __device__ __forceinline__ uint32_t u32(const uint8_t* p) {
+    if constexpr (kAligned) return *reinterpret_cast<const uint32_t*>(p);
+    return ld_u16(p) | (ld_u16(p + 2) << 16);
+  }
+};
+
 // ksigns(i) = i | parity(i) << 7 (the reference's ksigns_iq2xs table).
 __device__ __forceinline__ uint32_t ksigns7(uint32_t i) {
   return i | ((__popc(i) & 1u) << 7);
@@ -93,32 +112,35 @@ struct SubBlock {
   float dl[4];
 };
 
-template <int V>
+template <int V, bool kAligned = false>
 __device__ __forceinline__ SubBlock decode_sub_block(const uint8_t* q, const uint8_t* sc, float d,
                                                      uint32_t ib32, const uint64_t* grid) {
+  using L = Ld<kAligned>;
   SubBlock s;
   if constexpr (V == 1) {
     const uint32_t sbyte = sc[2 + ib32];
     const float dl0 = (d * (0.5f + (float)(sbyte & 0x0Fu))) * 0.25f;
     const float dl1 = (d * (0.5f + (float)(sbyte >> 4))) * 0.25f;
+    const uint32_t w01 = L::u32(q + 8 * ib32), w23 = L::u32(q + 8 * ib32 + 4);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const uint32_t qw = ld_u16(q + 8 * ib32 + 2 * w);
+      const uint32_t qw = ((w < 2 ? w01 : w23) >> (16 * (w & 1))) & 0xFFFFu;
       s.mag[w] = grid[qw & 0x1FFu];
       s.sgn[w] = ksigns7((qw >> 9) & 0x7Fu);
       s.dl[w] = w < 2 ? dl0 : dl1;
     }
   } else if constexpr (V == 2) {
     const uint32_t qh = q[64 + ib32], sbyte = sc[2 + ib32];
+    const uint32_t qs4 = L::u32(q + 4 * ib32), sg4 = L::u32(q + 32 + 4 * ib32);
 #pragma unroll
     for (int il = 0; il < 2; ++il) {
       const uint32_t nib = qh >> (4 * il);
       const float dl = (d * (0.5f + (float)((sbyte >> (4 * il)) & 0x0Fu))) * 0.25f;
-      const uint32_t off = 4 * ib32 + 2 * il;
-      s.mag[2 * il] = grid[q[off] | ((nib << 8) & 0x300u)];
-      s.mag[2 * il + 1] = grid[q[off + 1] | ((nib << 6) & 0x300u)];
-      s.sgn[2 * il] = q[32 + off];
-      s.sgn[2 * il + 1] = q[32 + off + 1];
+      const uint32_t b0 = (qs4 >> (16 * il)) & 0xFFu, b1 = (qs4 >> (16 * il + 8)) & 0xFFu;
+      s.mag[2 * il] = grid[b0 | ((nib << 8) & 0x300u)];
+      s.mag[2 * il + 1] = grid[b1 | ((nib << 6) & 0x300u)];
+      s.sgn[2 * il] = (sg4 >> (16 * il)) & 0xFFu;
+      s.sgn[2 * il + 1] = (sg4 >> (16 * il + 8)) & 0xFFu;
       s.dl[2 * il] = dl;
       s.dl[2 * il + 1] = dl;
     }
@@ -126,12 +148,15 @@ __device__ __forceinline__ SubBlock decode_sub_block(const uint8_t* q, const uin
     const uint32_t qh = q[64 + ib32];
     const uint32_t nib = (sc[2 + ib32 / 2] >> (4 * (ib32 & 1))) & 0x0Fu;
     const float dl = d * (1.0f + 2.0f * (float)nib);
+    const uint32_t lo = L::u32(q + 8 * ib32), hi = L::u32(q + 8 * ib32 + 4);
+    const uint32_t sg4 = L::u32(q + 72 + 4 * ib32);
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-      const uint32_t i1 = q[8 * ib32 + 2 * l] | (((qh >> (2 * l)) & 1u) << 8);
-      const uint32_t i2 = q[8 * ib32 + 2 * l + 1] | (((qh >> (2 * l + 1)) & 1u) << 8);
+      const uint32_t w = l < 2 ? lo : hi;
+      const uint32_t i1 = ((w >> (16 * (l & 1))) & 0xFFu) | (((qh >> (2 * l)) & 1u) << 8);
+      const uint32_t i2 = ((w >> (16 * (l & 1) + 8)) & 0xFFu) | (((qh >> (2 * l + 1)) & 1u) << 8);
       s.mag[l] = grid[i1] | (grid[i2] << 32);
-      s.sgn[l] = q[72 + 4 * ib32 + l];
+      s.sgn[l] = (sg4 >> (8 * l)) & 0xFFu;
       s.dl[l] = dl;
     }
   }
@@ -142,6 +167,96 @@ __device__ __forceinline__ SubBlock decode_sub_block(const uint8_t* q, const uin
 __device__ __forceinline__ float group_weight(const SubBlock& s, int g, int j) {
   const float mag = s.dl[g] * (float)((s.mag[g] >> (8 * j)) & 0xFFu);
   return ((s.sgn[g] >> j) & 1u) ? -mag : mag;
+}
+
+// Staged activation column c of row mm: 36 floats per 32 columns.
+__device__ __forceinline__ uint32_t xs_index(uint32_t mm, uint32_t c, uint32_t pitch) {
+  return mm * pitch + c + (c >> 5) * 4;
+}
+
+template <int V, bool kAligned>
+__global__ __launch_bounds__(256) void iq_variant_matmul_lds_kernel(
+    const void* x, int x_dtype, uint32_t m, const uint8_t* wb, const uint8_t* ws, float* out,
+    uint32_t out_dim, uint32_t in_dim, uint32_t bpr, const float* row_inv, uint32_t mc_max) {
+  using F = VariantFmt<V>;
+  __shared__ uint64_t grid[F::kGrid];
+  extern __shared__ __align__(16) float xs[];
+  build_variant_grid<V>(grid);
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t nsb = bpr * kSubBlocksPerBlock;
+  const uint32_t pitch = nsb * 36;  // staged floats per activation row
+  for (uint32_t m0 = 0; m0 < m; m0 += mc_max) {
+    const uint32_t mc = m - m0 < mc_max ? m - m0 : mc_max;
+    __syncthreads();  // the previous rows' readers are done
+    // eight loads in flight per thread before their stores
+    const uint32_t total = mc * in_dim;
+    for (uint32_t base = threadIdx.x; base < total; base += 8 * blockDim.x) {
+      float xv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t i = base + u * blockDim.x;
+        xv[u] = i < total ? load_x(x, x_dtype, (size_t)m0 * in_dim + i) : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t i = base + u * blockDim.x;
+        if (i < total) {
+          const uint32_t mm = i / in_dim, c = i - mm * in_dim;
+          xs[xs_index(mm, c, pitch)] = row_inv ? qdq_w8a8(xv[u], row_inv[m0 + mm]) : xv[u];
+        }
+      }
+    }
+    __syncthreads();
+    for (uint32_t r0 = (blockIdx.x * 4 + wave) * 4; r0 < out_dim; r0 += gridDim.x * 16) {
+      float acc[4][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) acc[r][mm] = 0.0f;
+      for (uint32_t sb = lane; sb < nsb; sb += 64) {
+        const uint32_t col0 = sb * 32;
+        if (col0 >= in_dim) continue;
+        SubBlock s[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t row = r0 + r < out_dim ? r0 + r : out_dim - 1;
+          const size_t block = (size_t)row * bpr + sb / 8;
+          const uint8_t* q = wb + block * F::kBytes;
+          const uint8_t* sc = ws + block * F::kScales;
+          s[r] = decode_sub_block<V, kAligned>(
+              q, sc, half_bits_to_float((uint16_t)Ld<kAligned>::u16(sc)), sb % 8, grid);
+        }
+        const uint32_t ncol = in_dim - col0 < 32 ? in_dim - col0 : 32;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+          for (int mm = 0; mm < 4; ++mm) {
+            if ((uint32_t)mm >= mc) break;
+            // eight staged activations of this group (zero past in_dim)
+            float xv[8];
+            const float* xp = xs + xs_index(mm, col0 + 8 * g, pitch);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xv[j] = (uint32_t)(8 * g + j) < ncol ? xp[j] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+              for (int j = 0; j < 8; ++j) acc[r][mm] = fmaf(xv[j], group_weight(s[r], g, j), acc[r][mm]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm) {
+          float v = acc[r][mm];
+#pragma unroll
+          for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+          if (lane == 0 && r0 + r < out_dim && (uint32_t)mm < mc)
+            out[(size_t)(m0 + mm) * out_dim + r0 + r] = v;
+        }
+    }
+  }
 }
 
 template <int V>
@@ -247,12 +362,38 @@ __global__ __launch_bounds__(256) void iq_variant_dequant_kernel(const uint8_t* 
   }
 }
 
+// LDS for the staged activation rows: at most 128 KB next to the codebook.
+constexpr size_t kVariantStageLimit = 128 * 1024;
+
 template <int V>
 static hipError_t launch_matmul_v(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                   const uint8_t* ws, float* out, uint32_t out_dim,
                                   uint32_t in_dim, const float* row_inv, int num_cus,
                                   hipStream_t stream) {
   const uint32_t bpr = (in_dim + kQK - 1) / kQK;
+  const size_t row_bytes = (size_t)bpr * kSubBlocksPerBlock * 36 * sizeof(float);
+  if (row_bytes <= kVariantStageLimit) {
+    uint32_t mc = (uint32_t)(kVariantStageLimit / row_bytes);
+    if (mc > 4) mc = 4;
+    if (mc > m) mc = m;
+    const bool al = reinterpret_cast<uintptr_t>(wb) % 4 == 0 &&
+                    reinterpret_cast<uintptr_t>(ws) % 2 == 0;
+    auto kern = al ? &iq_variant_matmul_lds_kernel<V, true> : &iq_variant_matmul_lds_kernel<V, false>;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[al]) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)kVariantStageLimit);
+      if (e != hipSuccess) return e;
+      attr_set[al] = true;
+    }
+    uint32_t blocks = (out_dim + 15) / 16;
+    const uint32_t cap = (uint32_t)num_cus * 4;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), (size_t)mc * row_bytes, stream, x, x_dtype,
+                       m, wb, ws, out, out_dim, in_dim, bpr, row_inv, mc);
+    return hipGetLastError();
+  }
   uint32_t blocks = (out_dim + 3) / 4;
   const uint32_t cap = (uint32_t)num_cus * 8;
   if (blocks > cap) blocks = cap;
