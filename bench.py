@@ -243,6 +243,37 @@ def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
     return res
 
 
+def bench_gguf_split(pkg, torch, stream, steps, k=4096, n=14336):
+    """GGUF (ggml) IQ2_XXS blocks of the gate matrix split into the reference's
+    pair: bytes moved (read + written) per launch over its duration."""
+    cabi = pkg.cabi
+    dev = torch.device("cuda:0")
+    sh = int(stream.cuda_stream)
+    nb = n * math.ceil(k / 256)
+    src = torch.randint(0, 256, (nb * 66,), dtype=torch.uint8, device=dev)
+    wb = torch.empty(nb * 64, dtype=torch.uint8, device=dev)
+    ws = torch.empty(nb * 2, dtype=torch.uint8, device=dev)
+
+    def call():
+        cabi.split_gguf_raw(src.data_ptr(), src.numel(), nb, cabi.CMK_IQ2_XXS, wb.data_ptr(),
+                            wb.numel(), ws.data_ptr(), ws.numel(), sh)
+
+    call()
+    torch.cuda.synchronize()
+    start, stop = cabi.Event(), cabi.Event()
+    start.record(sh)
+    for _ in range(steps):
+        call()
+    stop.record(sh)
+    torch.cuda.synchronize()
+    us = start.elapsed_ms(stop) * 1e3 / steps
+    moved = 2 * nb * 66
+    log(f"[bench] gguf split: {us:.2f} us per launch, {moved / (us * 1e-6) / 1e9:.1f} GB/s")
+    return {"variant": "iq2_xxs", "blocks": nb, "mean_launch_us": us, "bytes_moved": moved,
+            "gbs": moved / (us * 1e-6) / 1e9, "launches": steps,
+            "kernel": "cmk::gguf_split_kernel"}
+
+
 def cpu_baseline(pkg, seconds):
     """The oracle (scalar restatement of the reference's CPU reference, OpenMP over
     outputs) on the same decode step; repeated until `seconds` of CPU time."""
@@ -337,6 +368,7 @@ def main():
                    else bench_prefill(pkg, torch, stream, args.prefill_steps, 5))
         variants = (None if args.no_variants
                     else bench_variants(pkg, torch, stream, args.variant_steps))
+        split = None if args.no_variants else bench_gguf_split(pkg, torch, stream, 50)
     torch.cuda.synchronize()
     value = dec["step_bytes"] * args.steps / (dec["ms"] / 1e3) / 1e9
     achieved = dec["per_launch_bytes"] / (dec["mean_launch_us"] * 1e-6) / 1e9
@@ -374,6 +406,8 @@ def main():
         line["prefill_m512"] = prefill
     if variants is not None:
         line["variants_m1"] = variants
+    if split is not None:
+        line["gguf_split"] = split
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(pkg, args.cpu_seconds)
     else:

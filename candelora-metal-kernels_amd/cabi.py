@@ -29,6 +29,7 @@ EXPORTED = (
     "cmk_iq2_matmul",
     "cmk_iq2_matmul_workspace_size",
     "cmk_iq2_dequantize",
+    "cmk_iq2_split_gguf_blocks",
     "cmk_last_error",
     "cmk_abi_version",
     "cmk_iq2_matmul_path",
@@ -77,6 +78,8 @@ def lib() -> ctypes.CDLL:
     L.cmk_iq2_matmul_workspace_size.argtypes = [I, S, S, S, I, I, ctypes.POINTER(S)]
     L.cmk_iq2_matmul_workspace_size.restype = I
     L.cmk_iq2_dequantize.argtypes = [P, S, P, S, S, S, I, I, P, P]
+    L.cmk_iq2_split_gguf_blocks.argtypes = [P, S, S, I, P, S, P, S, P]
+    L.cmk_iq2_split_gguf_blocks.restype = I
     L.cmk_iq2_dequantize.restype = I
     L.cmk_last_error.argtypes = []
     L.cmk_last_error.restype = ctypes.c_char_p
@@ -126,6 +129,12 @@ def workspace_size(x_dtype, m, out_dim, in_dim, variant=CMK_IQ2_XXS,
     check(lib().cmk_iq2_matmul_workspace_size(x_dtype, m, out_dim, in_dim, variant, mode,
                                               ctypes.byref(n)))
     return n.value
+
+
+def split_gguf_raw(blocks_ptr, blocks_len, n_blocks, variant, wb_ptr, wb_len, ws_ptr, ws_len,
+                   stream=None) -> None:
+    check(lib().cmk_iq2_split_gguf_blocks(blocks_ptr, blocks_len, n_blocks, variant, wb_ptr,
+                                          wb_len, ws_ptr, ws_len, stream))
 
 
 def dequantize_raw(wb_ptr, wb_len, ws_ptr, ws_len, out_dim, in_dim, out_ptr,

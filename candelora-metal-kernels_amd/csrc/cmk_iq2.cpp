@@ -329,6 +329,41 @@ int cmk_iq2_dequantize(const uint8_t* weight_bytes, size_t weight_bytes_len,
   return ok();
 }
 
+int cmk_iq2_split_gguf_blocks(const uint8_t* blocks, size_t blocks_len, size_t n_blocks,
+                              cmk_iq2_variant variant, uint8_t* weight_bytes,
+                              size_t weight_bytes_len, uint8_t* weight_scales,
+                              size_t weight_scales_len, void* stream) {
+  if ((int)variant < CMK_IQ2_XXS || (int)variant > CMK_IQ3_S)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "invalid iq2 variant: %d", (int)variant);
+  const size_t cb = bytes_per_block((int)variant), sb = scales_per_block((int)variant);
+  size_t need_src, need_b, need_s;
+  if (!checked_mul(n_blocks, cb + sb, &need_src) || !checked_mul(n_blocks, cb, &need_b) ||
+      !checked_mul(n_blocks, sb, &need_s))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "split_gguf_blocks size overflow");
+  if (blocks_len < need_src)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "split_gguf_blocks blocks too small: got %zu expected at least %zu", blocks_len,
+                need_src);
+  if (weight_bytes_len < need_b)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "split_gguf_blocks weight_bytes too small: got %zu expected at least %zu",
+                weight_bytes_len, need_b);
+  if (weight_scales_len < need_s)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "split_gguf_blocks weight_scales too small: got %zu expected at least %zu",
+                weight_scales_len, need_s);
+  if (n_blocks == 0) return ok();
+  if (!blocks || !weight_bytes || !weight_scales)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "split_gguf_blocks null pointer argument");
+  int cus = 0;
+  int rc = current_cu_count(&cus);
+  if (rc != CMK_OK) return rc;
+  hipError_t e = cmk::launch_gguf_split(blocks, n_blocks, (uint32_t)cb, (uint32_t)sb, weight_bytes,
+                                        weight_scales, cus, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "split_gguf_blocks launch");
+  return ok();
+}
+
 // ---- runtime wrappers -----------------------------------------------------
 
 int cmk_device_count(int* count) {

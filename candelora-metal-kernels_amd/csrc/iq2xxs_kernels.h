@@ -59,4 +59,10 @@ hipError_t launch_iq_variant_dequant(int variant, const uint8_t* wb, const uint8
                                      int out_kind, uint32_t out_dim, uint32_t in_dim, int num_cus,
                                      hipStream_t stream);
 
+// GGUF (ggml) blocks of code_bytes + scale_bytes bytes each -> weight_bytes
+// (codes) and weight_scales (d, then the packed scales).  Any alignment.
+hipError_t launch_gguf_split(const uint8_t* blocks, uint64_t n_blocks, uint32_t code_bytes,
+                             uint32_t scale_bytes, uint8_t* wb, uint8_t* ws, int num_cus,
+                             hipStream_t stream);
+
 }  // namespace cmk

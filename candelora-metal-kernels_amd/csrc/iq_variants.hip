@@ -458,4 +458,63 @@ hipError_t launch_iq_variant_dequant(int variant, const uint8_t* wb, const uint8
   }
 }
 
+// ---------------------------------------------------------------------------
+// GGUF (ggml) blocks -> the reference's split pair.  A ggml block stores the
+// fp16 d first, then the code bytes, then the packed scales (none for
+// IQ2_XXS); weight_scales receives d and the scales, weight_bytes the codes.
+// Code bytes are gathered a dword per thread (code_bytes is a multiple of 4,
+// so a dword never straddles blocks; neighbouring threads read neighbouring
+// bytes), then scale bytes one per thread.  kAligned: weight_bytes is 4-byte
+// aligned and takes dword stores.
+// ---------------------------------------------------------------------------
+template <bool kAligned>
+__global__ __launch_bounds__(256) void gguf_split_kernel(const uint8_t* __restrict__ src,
+                                                         uint64_t n_blocks, uint32_t code_bytes,
+                                                         uint32_t scale_bytes,
+                                                         uint8_t* __restrict__ wb,
+                                                         uint8_t* __restrict__ ws) {
+  const uint64_t gb = code_bytes + scale_bytes;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t n_words = n_blocks * (code_bytes / 4);
+  for (uint64_t t = tid; t < n_words; t += stride) {
+    const uint64_t o = 4 * t;
+    const uint64_t b = o / code_bytes;
+    const uint8_t* s = src + b * gb + 2 + (o - b * code_bytes);
+    const uint32_t v = (uint32_t)s[0] | ((uint32_t)s[1] << 8) | ((uint32_t)s[2] << 16) |
+                       ((uint32_t)s[3] << 24);
+    if constexpr (kAligned) {
+      *reinterpret_cast<uint32_t*>(wb + o) = v;
+    } else {
+      wb[o] = (uint8_t)v;
+      wb[o + 1] = (uint8_t)(v >> 8);
+      wb[o + 2] = (uint8_t)(v >> 16);
+      wb[o + 3] = (uint8_t)(v >> 24);
+    }
+  }
+  const uint64_t n_sc = n_blocks * scale_bytes;
+  for (uint64_t t = tid; t < n_sc; t += stride) {
+    const uint64_t b = t / scale_bytes;
+    const uint32_t jb = (uint32_t)(t - b * scale_bytes);
+    ws[t] = src[b * gb + (jb < 2 ? jb : code_bytes + jb)];
+  }
+}
+
+hipError_t launch_gguf_split(const uint8_t* blocks, uint64_t n_blocks, uint32_t code_bytes,
+                             uint32_t scale_bytes, uint8_t* wb, uint8_t* ws, int num_cus,
+                             hipStream_t stream) {
+  const uint64_t work = n_blocks * (code_bytes / 4);
+  uint64_t grid = (work + 255) / 256;
+  const uint64_t cap = (uint64_t)num_cus * 32;
+  if (grid > cap) grid = cap;
+  if (grid == 0) grid = 1;
+  if (reinterpret_cast<uintptr_t>(wb) % 4 == 0)
+    hipLaunchKernelGGL(gguf_split_kernel<true>, dim3((uint32_t)grid), dim3(256), 0, stream,
+                       blocks, n_blocks, code_bytes, scale_bytes, wb, ws);
+  else
+    hipLaunchKernelGGL(gguf_split_kernel<false>, dim3((uint32_t)grid), dim3(256), 0, stream,
+                       blocks, n_blocks, code_bytes, scale_bytes, wb, ws);
+  return hipGetLastError();
+}
+
 }  // namespace cmk

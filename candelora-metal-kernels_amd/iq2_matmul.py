@@ -146,6 +146,38 @@ def iq2_dequantize_to_f16(weight_bytes, weight_scales, out_dim, in_dim, variant,
     return out
 
 
+# bytes / scales per 256-weight block (src/iq2_matmul.rs:13-29)
+_BLOCK_SIZES = {Iq2MatmulVariant.Iq2Xxs: (64, 2), Iq2MatmulVariant.Iq2Xs: (64, 10),
+                Iq2MatmulVariant.Iq2S: (72, 10), Iq2MatmulVariant.Iq3S: (104, 6)}
+
+
+def iq2_split_gguf_blocks(blocks, variant):
+    """GGUF (ggml) blocks -> (weight_bytes, weight_scales), the split pair the
+    matmul and dequantisation take (src/iq2_matmul.rs:13-17).  `blocks` is a flat
+    U8 device tensor of whole ggml blocks ({d; codes; scales}: 66, 74, 82 or 110
+    bytes).  No counterpart in the reference, whose callers split the blocks
+    themselves."""
+    variant = Iq2MatmulVariant(variant)
+    if blocks.device.type != "cuda":
+        raise Iq2MatmulError("split_gguf_blocks requires a HIP device")
+    if blocks.dtype != torch.uint8 or not blocks.is_contiguous():
+        raise Iq2MatmulError("split_gguf_blocks expects a contiguous U8 tensor")
+    cb, sb = _BLOCK_SIZES[variant]
+    if blocks.numel() % (cb + sb):
+        raise Iq2MatmulError(
+            f"split_gguf_blocks: {blocks.numel()} bytes is not a whole number of "
+            f"{cb + sb}-byte blocks")
+    n = blocks.numel() // (cb + sb)
+    wb = torch.empty(n * cb, dtype=torch.uint8, device=blocks.device)
+    ws = torch.empty(n * sb, dtype=torch.uint8, device=blocks.device)
+    try:
+        cabi.split_gguf_raw(blocks.data_ptr(), blocks.numel(), n, int(variant), wb.data_ptr(),
+                            wb.numel(), ws.data_ptr(), ws.numel(), _stream(blocks))
+    except cabi.CmkError as e:
+        raise Iq2MatmulError(str(e)) from None
+    return wb, ws
+
+
 def iq2_xxs_matmul(x, weight_bytes, weight_scales, out_dim, in_dim):
     return iq2_matmul(x, weight_bytes, weight_scales, out_dim, in_dim, Iq2MatmulVariant.Iq2Xxs)
 

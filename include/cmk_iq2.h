@@ -1,5 +1,5 @@
 /*
- * cmk_iq2.h — C ABI of the MI355X (gfx950) IQ2_XXS matmul library, libcmk_iq2.so.
+ * cmk_iq2.h — C ABI of the MI355X (gfx950) IQ2 matmul library, libcmk_iq2.so.
  *
  * This is the drop-in boundary for the crate candelora-metal-kernels: the
  * crate keeps its public Rust API (module candelora_metal_kernels::iq2_matmul,
@@ -72,11 +72,13 @@ typedef enum cmk_act_quant_mode {
 /* ------------------------------------------------------------------------ */
 
 /*
- * out[m, out_dim] (fp32) = x[m, in_dim] . W^T, W the IQ2_XXS matrix
- * [out_dim, in_dim] held as the reference's split super-blocks:
- *   weight_bytes : out_dim * ceil(in_dim/256) blocks x 64 B (32 x u16 qs)
- *   weight_scales: out_dim * ceil(in_dim/256) blocks x 2 B (fp16 d, LE)
- * (src/iq2_matmul.rs:13-17; block index = row * blocks_per_row + blk).
+ * out[m, out_dim] (fp32) = x[m, in_dim] . W^T, W the matrix [out_dim, in_dim]
+ * in format `variant`, held as the reference's split super-blocks:
+ *   weight_bytes : out_dim * ceil(in_dim/256) blocks x bytes_per_block
+ *                  (IQ2_XXS: 64 B, 32 x u16 qs)
+ *   weight_scales: out_dim * ceil(in_dim/256) blocks x scales_per_block
+ *                  (IQ2_XXS: 2 B, fp16 d, LE)
+ * (src/iq2_matmul.rs:13-29; block index = row * blocks_per_row + blk).
  *
  * Replaces iq2_matmul_metal (src/iq2_matmul.rs:197-365) as reached from
  * iq2_matmul / iq2_xxs_matmul (:535-553, :604-619) with mode OFF, and from
@@ -122,6 +124,21 @@ int cmk_iq2_dequantize(const uint8_t *weight_bytes, size_t weight_bytes_len,
                        const uint8_t *weight_scales, size_t weight_scales_len,
                        size_t out_dim, size_t in_dim, cmk_iq2_variant variant,
                        cmk_dtype out_dtype, void *out, void *stream);
+
+/*
+ * Splits n_blocks GGUF (ggml) blocks of `variant` into the reference's pair:
+ * weight_bytes (the code bytes, bytes_per_block each) and weight_scales (the
+ * fp16 d, then the packed scales; scales_per_block each).  A ggml block is
+ * {d; codes; scales}: 66, 74, 82 or 110 bytes for IQ2_XXS, IQ2_XS, IQ2_S,
+ * IQ3_S (ggml's block_iq2_xxs / block_iq2_xs / block_iq2_s / block_iq3_s).
+ * No counterpart in the reference, which expects callers to have split the
+ * blocks already (src/iq2_matmul.rs:13-17); it is the on-disk format step for
+ * GGUF weights.  Device pointers, any alignment, asynchronous on `stream`.
+ */
+int cmk_iq2_split_gguf_blocks(const uint8_t *blocks, size_t blocks_len, size_t n_blocks,
+                              cmk_iq2_variant variant, uint8_t *weight_bytes,
+                              size_t weight_bytes_len, uint8_t *weight_scales,
+                              size_t weight_scales_len, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Errors and introspection                                                  */

@@ -342,3 +342,23 @@ void oracle_iq_matmul_f64(int variant, const float *x, size_t m, size_t out_dim,
     }
     free(w);
 }
+
+/* ---- GGUF block layout ---------------------------------------------------- */
+
+size_t oracle_gguf_block_bytes(int variant) {
+    size_t b = oracle_iq_bytes_per_block(variant), s = oracle_iq_scales_per_block(variant);
+    return b ? b + s : 0;
+}
+
+void oracle_gguf_to_split(int variant, const uint8_t *blocks, size_t n_blocks,
+                          uint8_t *weight_bytes, uint8_t *weight_scales) {
+    const size_t bb = oracle_iq_bytes_per_block(variant), sb = oracle_iq_scales_per_block(variant);
+    const size_t gb = bb + sb;
+    for (size_t i = 0; i < n_blocks; ++i) {
+        const uint8_t *src = blocks + i * gb;
+        uint8_t *ws = weight_scales + i * sb;
+        memcpy(ws, src, 2);                             /* d */
+        memcpy(weight_bytes + i * bb, src + 2, bb);     /* codes */
+        memcpy(ws + 2, src + 2 + bb, sb - 2);           /* packed scales (none for IQ2_XXS) */
+    }
+}

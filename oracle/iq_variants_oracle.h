@@ -60,6 +60,21 @@ void oracle_iq_dequantize_bf16(int variant, const uint8_t *weight_bytes,
                                const uint8_t *weight_scales, size_t out_dim, size_t in_dim,
                                uint16_t *out);
 
+/* GGUF (ggml) block layout to the reference's split pair (src/iq2_matmul.rs:
+ * 13-17: weight_bytes + weight_scales).  ggml's block structs (ggml-common.h,
+ * the format the reference's tables come from, iq2_tables.metal:1-2) store,
+ * per 256-weight block, the fp16 d first, then the code bytes, then (IQ2_XS,
+ * IQ2_S, IQ3_S) the packed 4-bit scales last:
+ *   iq2_xxs {d; qs[64]}                        66 B -> 64 + 2
+ *   iq2_xs  {d; qs[64]; scales[8]}             74 B -> 64 + 10
+ *   iq2_s   {d; qs[64]; qh[8]; scales[8]}      82 B -> 72 + 10
+ *   iq3_s   {d; qs[64]; qh[8]; signs[32]; scales[4]}  110 B -> 104 + 6
+ * weight_scales = d followed by the scales; weight_bytes = everything between.
+ * Returns the GGUF block size, 0 for an unknown variant. */
+size_t oracle_gguf_block_bytes(int variant);
+void oracle_gguf_to_split(int variant, const uint8_t *blocks, size_t n_blocks,
+                          uint8_t *weight_bytes, uint8_t *weight_scales);
+
 /* Error-metric helper (not a restatement): fp64 accumulation of the decoded
  * products plus the condition scale sum_k |x_k * w_nk|, both [m, out_dim]. */
 void oracle_iq_matmul_f64(int variant, const float *x, size_t m, size_t out_dim, size_t in_dim,

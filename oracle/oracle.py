@@ -68,6 +68,9 @@ def lib():
         L.oracle_iq_dequantize_f16.argtypes = [I, P, P, S, S, P]
         L.oracle_iq_dequantize_bf16.argtypes = [I, P, P, S, S, P]
         L.oracle_iq_matmul_f64.argtypes = [I, P, S, S, S, P, P, P, P]
+        L.oracle_gguf_block_bytes.argtypes = [I]
+        L.oracle_gguf_block_bytes.restype = S
+        L.oracle_gguf_to_split.argtypes = [I, P, S, P, P]
         _lib = L
     return _lib
 
@@ -252,6 +255,19 @@ def variant_matmul_f64(variant, x, m, out_dim, in_dim, wb, ws):
     sc = np.zeros((m, out_dim), np.float64)
     lib().oracle_iq_matmul_f64(variant, _p(x), m, out_dim, in_dim, _p(wb), _p(ws), _p(out), _p(sc))
     return out, sc
+
+
+def gguf_block_bytes(variant: int) -> int:
+    return lib().oracle_gguf_block_bytes(variant)
+
+
+def gguf_to_split(variant, blocks, n_blocks):
+    """ggml AoS blocks -> (weight_bytes, weight_scales) as the reference splits them."""
+    blocks = _u8(blocks)
+    wb = np.zeros(n_blocks * bytes_per_block(variant), np.uint8)
+    ws = np.zeros(n_blocks * scales_per_block(variant), np.uint8)
+    lib().oracle_gguf_to_split(variant, _p(blocks), n_blocks, _p(wb), _p(ws))
+    return wb, ws
 
 
 def reference_case_inputs(m=2, out_dim=7, in_dim=320, bytes_seed=0xA11CE5ED,

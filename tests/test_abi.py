@@ -155,3 +155,24 @@ def test_workspace_and_path_queries(cabi):
     assert cabi.matmul_path(cabi.CMK_F32, 1, 14336, 4096) == "gemv"
     with pytest.raises(cabi.CmkError):
         cabi.workspace_size(cabi.CMK_F16, 1, 0, 4096)
+
+
+def test_split_gguf_blocks_argument_errors(cabi):
+    L = cabi.lib()
+
+    def sp(**kw):
+        a = dict(src=NULL, sl=0, n=3, v=1, wb=NULL, wbl=1 << 20, ws=NULL, wsl=1 << 20)
+        a.update(kw)
+        rc = L.cmk_iq2_split_gguf_blocks(a["src"], a["sl"], a["n"], a["v"], a["wb"], a["wbl"],
+                                         a["ws"], a["wsl"], NULL)
+        return rc, cabi.last_error()
+
+    assert sp(v=7)[1] == "invalid iq2 variant: 7"
+    assert sp(sl=221)[1] == "split_gguf_blocks blocks too small: got 221 expected at least 222"
+    assert sp(sl=222, wbl=191)[1] == ("split_gguf_blocks weight_bytes too small: got 191 expected "
+                                      "at least 192")
+    assert sp(sl=222, wsl=29)[1] == ("split_gguf_blocks weight_scales too small: got 29 expected "
+                                     "at least 30")
+    assert sp(sl=222)[1] == "split_gguf_blocks null pointer argument"
+    assert sp(n=0)[0] == cabi.CMK_OK
+

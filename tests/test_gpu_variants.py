@@ -153,3 +153,51 @@ def test_unaligned_weight_buffers(pkg, oracle, dev, v):
     d_al = pkg.iq2_dequantize_to_f16(to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim, ve)
     d_un = pkg.iq2_dequantize_to_f16(wbig[1:], sbig[1:], out_dim, in_dim, ve)
     assert torch.equal(d_al, d_un)
+
+
+@pytest.mark.parametrize("v", [0, XS, S, S3])
+@pytest.mark.parametrize("n_blocks", [1, 37, 4096 * 3 + 5])
+def test_split_gguf_blocks_bit_exact(pkg, oracle, dev, v, n_blocks):
+    gb = oracle.gguf_block_bytes(v)
+    raw = np.random.default_rng(v + n_blocks).integers(0, 256, n_blocks * gb, dtype=np.uint8)
+    wb, ws = pkg.iq2_split_gguf_blocks(to_dev(raw, dev), variant_enum(pkg, v))
+    ref_b, ref_s = oracle.gguf_to_split(v, raw, n_blocks)
+    assert np.array_equal(wb.cpu().numpy(), ref_b)
+    assert np.array_equal(ws.cpu().numpy(), ref_s)
+
+
+@pytest.mark.parametrize("v", [0, XS, S, S3])
+def test_gguf_blocks_to_matmul(pkg, oracle, dev, v):
+    """ggml blocks -> split on the GPU -> matmul equals the oracle on the
+    oracle's split of the same blocks."""
+    out_dim, in_dim, m = 11, 512, 2
+    n_blocks = out_dim * 2
+    gb = oracle.gguf_block_bytes(v)
+    rng = np.random.default_rng(300 + v)
+    raw = rng.integers(0, 256, n_blocks * gb, dtype=np.uint8)
+    raw[1::gb] = rng.integers(0x10, 0x20, n_blocks, dtype=np.uint8)  # d (bytes 0-1): finite
+    wb, ws = pkg.iq2_split_gguf_blocks(to_dev(raw, dev), variant_enum(pkg, v))
+    x = rng.standard_normal((m, in_dim)).astype(np.float32)
+    y = pkg.iq2_matmul(to_dev(x, dev), wb, ws, out_dim, in_dim, variant_enum(pkg, v))
+    rb, rs = oracle.gguf_to_split(v, raw, n_blocks)
+    y64, scale = oracle.variant_matmul_f64(v, x, m, out_dim, in_dim, rb, rs)
+    cond, rel = errors(y.cpu().numpy(), y64, scale)
+    assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+
+
+@pytest.mark.parametrize("v", [0, S3])
+def test_split_gguf_blocks_unaligned_outputs(pkg, cabi, oracle, dev, v):
+    """Outputs at odd addresses (byte stores) match the aligned split."""
+    n = 513
+    gb = oracle.gguf_block_bytes(v)
+    raw = np.random.default_rng(5 + v).integers(0, 256, n * gb, dtype=np.uint8)
+    src = to_dev(raw, dev)
+    cb, sb = oracle.bytes_per_block(v), oracle.scales_per_block(v)
+    wbig = torch.zeros(n * cb + 1, dtype=torch.uint8, device=dev)
+    sbig = torch.zeros(n * sb + 1, dtype=torch.uint8, device=dev)
+    cabi.split_gguf_raw(src.data_ptr(), src.numel(), n, v, wbig.data_ptr() + 1, n * cb,
+                        sbig.data_ptr() + 1, n * sb, None)
+    torch.cuda.synchronize()
+    ref_b, ref_s = oracle.gguf_to_split(v, raw, n)
+    assert np.array_equal(wbig[1:].cpu().numpy(), ref_b)
+    assert np.array_equal(sbig[1:].cpu().numpy(), ref_s)

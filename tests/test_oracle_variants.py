@@ -277,3 +277,53 @@ def test_matmul_w8a8_is_reference_on_qdq(oracle, v):
     y = oracle.variant_matmul_reference_w8a8(v, x, m, out_dim, in_dim, wb, ws)
     xq = oracle.rowwise_qdq_w8a8(x, m, in_dim)
     assert np.array_equal(y, oracle.variant_matmul_reference(v, xq, m, out_dim, in_dim, wb, ws))
+
+
+# ---- GGUF (ggml) block layout ----------------------------------------------------
+# ggml's block structs (ggml-common.h, QK_K = 256), restated as numpy structured
+# dtypes: the fp16 d first, then the codes, then the packed scales.
+GGUF_DTYPES = {
+    0: np.dtype([("d", "<u2"), ("qs", "u1", 64)]),
+    XS: np.dtype([("d", "<u2"), ("qs", "u1", 64), ("scales", "u1", 8)]),
+    S: np.dtype([("d", "<u2"), ("qs", "u1", 64), ("qh", "u1", 8), ("scales", "u1", 8)]),
+    S3: np.dtype([("d", "<u2"), ("qs", "u1", 64), ("qh", "u1", 8), ("signs", "u1", 32),
+                  ("scales", "u1", 4)]),
+}
+
+
+@pytest.mark.parametrize("v", [0, XS, S, S3])
+def test_gguf_block_sizes(oracle, v):
+    assert oracle.gguf_block_bytes(v) == GGUF_DTYPES[v].itemsize == {0: 66, XS: 74, S: 82,
+                                                                      S3: 110}[v]
+    assert oracle.gguf_block_bytes(v) == oracle.bytes_per_block(v) + oracle.scales_per_block(v)
+
+
+@pytest.mark.parametrize("v", [0, XS, S, S3])
+def test_gguf_split_fields(oracle, v):
+    """d and the packed scales go to weight_scales (d first, as the reference's
+    decoders read it, src/iq2_matmul.rs:857,888), the codes in struct order to
+    weight_bytes; assembling the blocks back from the pair is the identity."""
+    dt = GGUF_DTYPES[v]
+    n = 37
+    raw = np.random.default_rng(70 + v).integers(0, 256, n * dt.itemsize, dtype=np.uint8)
+    rec = raw.view(dt)
+    wb, ws = oracle.gguf_to_split(v, raw, n)
+    codes = [f for f in dt.names if f not in ("d", "scales")]
+    want_b = np.concatenate([np.concatenate([rec[f][i].ravel() for f in codes]) for i in range(n)])
+    assert np.array_equal(wb, want_b)
+    ws2 = ws.reshape(n, -1)
+    assert np.array_equal(ws2[:, :2].copy().view("<u2").ravel(), rec["d"])
+    if "scales" in dt.names:
+        assert np.array_equal(ws2[:, 2:], rec["scales"])
+    # inverse: rebuild the ggml blocks from the pair
+    back = np.zeros(n, dt)
+    back["d"] = ws2[:, :2].copy().view("<u2").ravel()
+    off = 0
+    wb2 = wb.reshape(n, -1)
+    for f in codes:
+        k = dt.fields[f][0].shape[0]
+        back[f] = wb2[:, off:off + k]
+        off += k
+    if "scales" in dt.names:
+        back["scales"] = ws2[:, 2:]
+    assert np.array_equal(back.view(np.uint8), raw)
