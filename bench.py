@@ -243,6 +243,59 @@ def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
     return res
 
 
+def bench_mlp_step(pkg, torch, stream, steps, k=4096, n=14336):
+    """One Llama-3-8B MLP decode step with its data dependency: g = gate(x),
+    u = up(x), h = silu(g) * u, y = down(h), over rotated weight copies."""
+    cabi, inputs = pkg.cabi, pkg.inputs
+    dev = torch.device("cuda:0")
+    sh = int(stream.cuda_stream)
+    step_w = sum(nn * math.ceil(kk / 256) * 66 for _, kk, nn in DECODE_SHAPES)
+    copies = max(2, math.ceil(2 * MALL_BYTES / step_w))
+    x = torch.from_numpy(inputs.synthetic_x(1, k)).to(dev)
+    g = torch.empty((1, n), dtype=torch.float32, device=dev)
+    u = torch.empty((1, n), dtype=torch.float32, device=dev)
+    h = torch.empty((1, n), dtype=torch.float32, device=dev)
+    y = torch.empty((1, k), dtype=torch.float32, device=dev)
+    sets = []
+    for name, kk, nn in DECODE_SHAPES:
+        wb, ws = inputs.synthetic_weights(nn, kk)
+        wbt, wst = torch.from_numpy(wb).to(dev), torch.from_numpy(ws).to(dev)
+        sets.append([(wbt, wst)] + [(wbt.clone(), wst.clone()) for _ in range(copies - 1)])
+    calls = []
+    for c in range(copies):
+        (gw, gs), (uw, us), (dw, ds) = sets[0][c], sets[1][c], sets[2][c]
+        calls.append((Matmul(cabi, x, gw, gs, g, 1, k, n, cabi.CMK_F32, sh),
+                      Matmul(cabi, x, uw, us, u, 1, k, n, cabi.CMK_F32, sh),
+                      Matmul(cabi, h, dw, ds, y, 1, n, k, cabi.CMK_F32, sh)))
+
+    def run(i):
+        gate, up, down = calls[i % copies]
+        gate()
+        up()
+        cabi.swiglu_raw(g.data_ptr(), u.data_ptr(), n, h.data_ptr(), cabi.CMK_F32, sh)
+        down()
+
+    for i in range(copies):
+        run(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            run(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = cabi.Event(), cabi.Event()
+    start.record(sh)
+    graph.replay()
+    stop.record(sh)
+    torch.cuda.synchronize()
+    us = start.elapsed_ms(stop) * 1e3 / steps
+    step_bytes = sum(alg_bytes(1, kk, nn) for _, kk, nn in DECODE_SHAPES) + n * 12
+    log(f"[bench] mlp step (gate, up, swiglu, down): {us:.2f} us per step")
+    return {"us_per_step": us, "launches_per_step": 4, "alg_bytes_per_step": step_bytes,
+            "gbs": step_bytes / (us * 1e-6) / 1e9, "steps": steps}
+
+
 def bench_gguf_split(pkg, torch, stream, steps, k=4096, n=14336):
     """GGUF (ggml) IQ2_XXS blocks of the gate matrix split into the reference's
     pair: bytes moved (read + written) per launch over its duration."""
@@ -369,6 +422,7 @@ def main():
         variants = (None if args.no_variants
                     else bench_variants(pkg, torch, stream, args.variant_steps))
         split = None if args.no_variants else bench_gguf_split(pkg, torch, stream, 50)
+        mlp = None if args.no_variants else bench_mlp_step(pkg, torch, stream, 300)
     torch.cuda.synchronize()
     value = dec["step_bytes"] * args.steps / (dec["ms"] / 1e3) / 1e9
     achieved = dec["per_launch_bytes"] / (dec["mean_launch_us"] * 1e-6) / 1e9
@@ -408,6 +462,8 @@ def main():
         line["variants_m1"] = variants
     if split is not None:
         line["gguf_split"] = split
+    if mlp is not None:
+        line["mlp_step_m1"] = mlp
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(pkg, args.cpu_seconds)
     else:

@@ -4,8 +4,8 @@ The compute path is libcmk_iq2.so (HIP kernels behind the C ABI in
 include/cmk_iq2.h).  This package gives Python callers the same surface as the
 reference crate's public API (iq2_matmul, iq2_matmul_with_activation_quant,
 iq2_dequantize_to_f16, Iq2MatmulVariant, ActivationQuantMode/Config) over
-PyTorch device tensors, plus the GGUF block split (iq2_split_gguf_blocks) and
-seeded input generators.
+PyTorch device tensors, plus the GGUF block split (iq2_split_gguf_blocks), the MLP's
+silu(gate) * up step (swiglu) and seeded input generators.
 """
 
 from . import cabi, inputs  # noqa: F401
@@ -21,6 +21,7 @@ from .iq2_matmul import (  # noqa: F401
     iq2_xs_matmul,
     iq2_xxs_matmul,
     iq3_s_matmul,
+    swiglu,
 )
 
 __all__ = [
@@ -36,4 +37,5 @@ __all__ = [
     "iq2_s_matmul",
     "iq3_s_matmul",
     "iq2_split_gguf_blocks",
+    "swiglu",
 ]

@@ -47,6 +47,7 @@ HIP_SOURCES = [
     "iq2xxs_gemm.hip",
     "iq2xxs_simple.hip",
     "iq_variants.hip",
+    "mlp_ops.hip",
     "cmk_iq2.cpp",
 ]
 

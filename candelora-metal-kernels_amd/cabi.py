@@ -30,6 +30,7 @@ EXPORTED = (
     "cmk_iq2_matmul_workspace_size",
     "cmk_iq2_dequantize",
     "cmk_iq2_split_gguf_blocks",
+    "cmk_swiglu",
     "cmk_last_error",
     "cmk_abi_version",
     "cmk_iq2_matmul_path",
@@ -80,6 +81,8 @@ def lib() -> ctypes.CDLL:
     L.cmk_iq2_dequantize.argtypes = [P, S, P, S, S, S, I, I, P, P]
     L.cmk_iq2_split_gguf_blocks.argtypes = [P, S, S, I, P, S, P, S, P]
     L.cmk_iq2_split_gguf_blocks.restype = I
+    L.cmk_swiglu.argtypes = [P, P, S, I, P, P]
+    L.cmk_swiglu.restype = I
     L.cmk_iq2_dequantize.restype = I
     L.cmk_last_error.argtypes = []
     L.cmk_last_error.restype = ctypes.c_char_p
@@ -135,6 +138,10 @@ def split_gguf_raw(blocks_ptr, blocks_len, n_blocks, variant, wb_ptr, wb_len, ws
                    stream=None) -> None:
     check(lib().cmk_iq2_split_gguf_blocks(blocks_ptr, blocks_len, n_blocks, variant, wb_ptr,
                                           wb_len, ws_ptr, ws_len, stream))
+
+
+def swiglu_raw(gate_ptr, up_ptr, n, out_ptr, out_dtype=CMK_F32, stream=None) -> None:
+    check(lib().cmk_swiglu(gate_ptr, up_ptr, n, out_dtype, out_ptr, stream))
 
 
 def dequantize_raw(wb_ptr, wb_len, ws_ptr, ws_len, out_dim, in_dim, out_ptr,

@@ -364,6 +364,23 @@ int cmk_iq2_split_gguf_blocks(const uint8_t* blocks, size_t blocks_len, size_t n
   return ok();
 }
 
+int cmk_swiglu(const float* gate, const float* up, size_t n, cmk_dtype out_dtype, void* out,
+               void* stream) {
+  if (out_dtype != CMK_F32 && out_dtype != CMK_F16 && out_dtype != CMK_BF16)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "swiglu unsupported output dtype: %d", (int)out_dtype);
+  if (n == 0) return ok();
+  if (!gate || !up || !out) return fail(CMK_ERR_INVALID_ARGUMENT, "swiglu null pointer argument");
+  if (!aligned(gate, 4) || !aligned(up, 4) || !aligned(out, out_dtype == CMK_F32 ? 4 : 2))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "swiglu buffers must be aligned to their element size");
+  int cus = 0;
+  int rc = current_cu_count(&cus);
+  if (rc != CMK_OK) return rc;
+  hipError_t e = cmk::launch_swiglu(gate, up, out, (int)out_dtype, n, cus,
+                                    static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "swiglu launch");
+  return ok();
+}
+
 // ---- runtime wrappers -----------------------------------------------------
 
 int cmk_device_count(int* count) {

@@ -65,4 +65,9 @@ hipError_t launch_gguf_split(const uint8_t* blocks, uint64_t n_blocks, uint32_t 
                              uint32_t scale_bytes, uint8_t* wb, uint8_t* ws, int num_cus,
                              hipStream_t stream);
 
+// h[i] = silu(gate[i]) * up[i] for i < n, written as f32 (out_kind 0), f16 (1)
+// or bf16 (2).  Any alignment.
+hipError_t launch_swiglu(const float* gate, const float* up, void* out, int out_kind, uint64_t n,
+                         int num_cus, hipStream_t stream);
+
 }  // namespace cmk

@@ -178,6 +178,25 @@ def iq2_split_gguf_blocks(blocks, variant):
     return wb, ws
 
 
+def swiglu(gate, up, out_dtype=torch.float32):
+    """h = silu(gate) * up elementwise (fp32 in, f32/f16/bf16 out): the step
+    between the gate/up and the down projection.  No counterpart in the
+    reference, whose callers compose it from candle ops."""
+    if gate.device.type != "cuda" or up.device != gate.device:
+        raise Iq2MatmulError("swiglu requires gate and up on one HIP device")
+    if gate.dtype != torch.float32 or up.dtype != torch.float32:
+        raise Iq2MatmulError("swiglu expects F32 gate and up")
+    if gate.shape != up.shape or not gate.is_contiguous() or not up.is_contiguous():
+        raise Iq2MatmulError("swiglu expects contiguous gate and up of one shape")
+    out = torch.empty(gate.shape, dtype=out_dtype, device=gate.device)
+    try:
+        cabi.swiglu_raw(gate.data_ptr(), up.data_ptr(), gate.numel(), out.data_ptr(),
+                        _DTYPES[out_dtype], _stream(gate))
+    except cabi.CmkError as e:
+        raise Iq2MatmulError(str(e)) from None
+    return out
+
+
 def iq2_xxs_matmul(x, weight_bytes, weight_scales, out_dim, in_dim):
     return iq2_matmul(x, weight_bytes, weight_scales, out_dim, in_dim, Iq2MatmulVariant.Iq2Xxs)
 

@@ -140,6 +140,18 @@ int cmk_iq2_split_gguf_blocks(const uint8_t *blocks, size_t blocks_len, size_t n
                               size_t weight_bytes_len, uint8_t *weight_scales,
                               size_t weight_scales_len, void *stream);
 
+/*
+ * out[i] = silu(gate[i]) * up[i], i < n, silu(g) = g / (1 + exp(-g)) in fp32;
+ * out in F32, F16 or BF16 (one round-to-nearest-even).  The step between the
+ * gate/up and down projections of a Llama-style MLP: gate and up are the fp32
+ * outputs of cmk_iq2_matmul, out feeds the down projection's cmk_iq2_matmul
+ * (F32 for the GEMV at small m, F16/BF16 for the MFMA GEMM).  No counterpart in
+ * the reference, whose callers compose it from candle ops.  Device pointers,
+ * asynchronous on `stream`.
+ */
+int cmk_swiglu(const float *gate, const float *up, size_t n, cmk_dtype out_dtype, void *out,
+               void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* Errors and introspection                                                  */
 /* ------------------------------------------------------------------------ */

@@ -176,3 +176,12 @@ def test_split_gguf_blocks_argument_errors(cabi):
     assert sp(sl=222)[1] == "split_gguf_blocks null pointer argument"
     assert sp(n=0)[0] == cabi.CMK_OK
 
+
+def test_swiglu_argument_errors(cabi):
+    L = cabi.lib()
+    assert L.cmk_swiglu(NULL, NULL, 4, 7, NULL, NULL) == cabi.CMK_ERR_INVALID_ARGUMENT
+    assert cabi.last_error() == "swiglu unsupported output dtype: 7"
+    assert L.cmk_swiglu(NULL, NULL, 4, 0, NULL, NULL) == cabi.CMK_ERR_INVALID_ARGUMENT
+    assert cabi.last_error() == "swiglu null pointer argument"
+    assert L.cmk_swiglu(NULL, NULL, 0, 0, NULL, NULL) == cabi.CMK_OK
+
