@@ -243,6 +243,92 @@ def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
     return res
 
 
+CONFIG4_SHAPES = [("q", 8192, 8192), ("k", 8192, 1024), ("v", 8192, 1024), ("o", 8192, 8192),
+                  ("gate", 8192, 28672), ("up", 8192, 28672), ("down", 28672, 8192)]
+
+
+def _timed_graph(torch, cabi, stream, sh, run, steps):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            run(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = cabi.Event(), cabi.Event()
+    start.record(sh)
+    graph.replay()
+    stop.record(sh)
+    torch.cuda.synchronize()
+    return start.elapsed_ms(stop) * 1e3 / steps  # microseconds per step
+
+
+def bench_configs(pkg, torch, stream):
+    """BASELINE config 2 (M in {4, 8, 16}, f32 x, %HBM) and config 4 (the
+    Llama-3-70B layer's seven projections back to back: M=1 with f32 x, M=128
+    with f16 x on the MFMA GEMM), over rotated weight copies."""
+    cabi, inputs = pkg.cabi, pkg.inputs
+    dev = torch.device("cuda:0")
+    sh = int(stream.cuda_stream)
+    res = {"config2": [], "config4": {}}
+    for k, n in ((4096, 4096), (4096, 14336)):
+        wb, ws = inputs.synthetic_weights(n, k)
+        w_bytes = wb.size + ws.size
+        copies = max(2, math.ceil(2 * MALL_BYTES / w_bytes))
+        wbt, wst = torch.from_numpy(wb).to(dev), torch.from_numpy(ws).to(dev)
+        reps = [(wbt, wst)] + [(wbt.clone(), wst.clone()) for _ in range(copies - 1)]
+        for m in (4, 8, 16):
+            x = torch.from_numpy(inputs.synthetic_x(m, k)).to(dev)
+            out = torch.empty((m, n), dtype=torch.float32, device=dev)
+            calls = [Matmul(cabi, x, r[0], r[1], out, m, k, n, cabi.CMK_F32, sh) for r in reps]
+            for c in calls:
+                c()
+            us = _timed_graph(torch, cabi, stream, sh, lambda i: calls[i % copies](), 100)
+            gbs = alg_bytes(m, k, n) / (us * 1e-6) / 1e9
+            res["config2"].append({"m": m, "k": k, "n": n, "us": us, "gbs": gbs,
+                                   "frac_of_hbm_peak": gbs / HBM_PEAK_GBS})
+            log(f"[bench] config 2 m={m} k={k} n={n}: {us:.2f} us, {gbs:.1f} GB/s")
+        del reps
+    layer_w = sum(nn * math.ceil(kk / 256) * 66 for _, kk, nn in CONFIG4_SHAPES)
+    copies = max(2, math.ceil(2 * MALL_BYTES / layer_w))
+    weights = []
+    for _, kk, nn in CONFIG4_SHAPES:
+        wb, ws = inputs.synthetic_weights(nn, kk)
+        wbt, wst = torch.from_numpy(wb).to(dev), torch.from_numpy(ws).to(dev)
+        weights.append([(wbt, wst)] + [(wbt.clone(), wst.clone()) for _ in range(copies - 1)])
+    for m, dt in ((1, "f32"), (128, "f16")):
+        calls = []
+        for j, (_, kk, nn) in enumerate(CONFIG4_SHAPES):
+            if dt == "f32":
+                x = torch.from_numpy(inputs.synthetic_x(m, kk)).to(dev)
+                xd = cabi.CMK_F32
+            else:
+                x = torch.from_numpy(inputs.synthetic_x(m, kk, dtype="f16").view("int16")).to(dev)
+                x = x.view(torch.float16)
+                xd = cabi.CMK_F16
+            out = torch.empty((m, nn), dtype=torch.float32, device=dev)
+            calls.append([Matmul(cabi, x, w[0], w[1], out, m, kk, nn, xd, sh) for w in weights[j]])
+
+        def run(i):
+            for per_proj in calls:
+                per_proj[i % copies]()
+
+        for i in range(copies):
+            run(i)
+        torch.cuda.synchronize()
+        us = _timed_graph(torch, cabi, stream, sh, run, 20)
+        xb = 4 if dt == "f32" else 2
+        ab = sum(alg_bytes(m, kk, nn, xb) for _, kk, nn in CONFIG4_SHAPES)
+        fl = sum(2.0 * m * kk * nn for _, kk, nn in CONFIG4_SHAPES)
+        entry = {"m": m, "x_dtype": dt, "us_per_layer": us, "alg_bytes": ab,
+                 "gbs": ab / (us * 1e-6) / 1e9, "tflops": fl / (us * 1e-6) / 1e12}
+        entry["frac_of_hbm_peak"] = entry["gbs"] / HBM_PEAK_GBS
+        entry["frac_of_mfma_peak"] = entry["tflops"] / MFMA_F16_PEAK_TFLOPS
+        res["config4"][f"m{m}"] = entry
+        log(f"[bench] config 4 m={m} ({dt}): {us:.1f} us per layer, {entry['gbs']:.1f} GB/s, "
+            f"{entry['tflops']:.1f} TFLOP/s")
+    return res
+
+
 def bench_mlp_step(pkg, torch, stream, steps, k=4096, n=14336):
     """One Llama-3-8B MLP decode step with its data dependency: g = gate(x),
     u = up(x), h = silu(g) * u, y = down(h), over rotated weight copies."""
@@ -381,6 +467,8 @@ def main():
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the IQ2_XS / IQ2_S / IQ3_S lines")
     ap.add_argument("--variant-steps", type=int, default=200)
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the BASELINE config 2 and config 4 lines")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -423,6 +511,7 @@ def main():
                     else bench_variants(pkg, torch, stream, args.variant_steps))
         split = None if args.no_variants else bench_gguf_split(pkg, torch, stream, 50)
         mlp = None if args.no_variants else bench_mlp_step(pkg, torch, stream, 300)
+        configs = None if args.no_configs else bench_configs(pkg, torch, stream)
     torch.cuda.synchronize()
     value = dec["step_bytes"] * args.steps / (dec["ms"] / 1e3) / 1e9
     achieved = dec["per_launch_bytes"] / (dec["mean_launch_us"] * 1e-6) / 1e9
@@ -464,6 +553,9 @@ def main():
         line["gguf_split"] = split
     if mlp is not None:
         line["mlp_step_m1"] = mlp
+    if configs is not None:
+        line["config2_small_m"] = configs["config2"]
+        line["config4_70b_layer"] = configs["config4"]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(pkg, args.cpu_seconds)
     else:
