@@ -85,9 +85,12 @@ enum class Path { Gemv, Gemm, Simple, Variant };
 Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, const void* x,
                  const void* wb, const void* ws) {
   auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; };
-  const bool half_x = x_dtype == CMK_F16 || x_dtype == CMK_BF16;
-  if (half_x && m > kGemvMaxM && m <= UINT32_MAX &&
-      cmk::gemm_supported((uint32_t)m, out_dim, in_dim) && al(x, 16) && al(wb, 16) && al(ws, 2))
+  // f32 rows beyond the GEMV's range are staged as scaled f16 head / tail row
+  // pairs for the GEMM (twice the rows).
+  const size_t gemm_rows = x_dtype == CMK_F32 ? 2 * m : m;
+  if (m > kGemvMaxM && gemm_rows <= UINT32_MAX &&
+      cmk::gemm_supported((uint32_t)gemm_rows, out_dim, in_dim) && al(x, 16) && al(wb, 16) &&
+      al(ws, 2))
     return Path::Gemm;
   if (m <= UINT32_MAX && cmk::gemv_supported((uint32_t)m, out_dim, in_dim, x_dtype) &&
       al(wb, 16) && al(ws, 2))
@@ -100,9 +103,14 @@ size_t row_scale_bytes(size_t m) {
   return ((m * sizeof(float) + kWorkspaceAlign - 1) / kWorkspaceAlign) * kWorkspaceAlign;
 }
 
-size_t workspace_for(Path p, bool w8a8, size_t m, uint32_t in_dim) {
-  if (!w8a8 || p == Path::Gemv) return 0;  // Simple and Variant: row scales only
-  if (p == Path::Gemm) return row_scale_bytes(m) + cmk::gemm_w8a8_scratch_bytes((uint32_t)m, in_dim);
+// The GEMM stages f32 rows (as head / tail pairs) and W8A8 rows in the
+// workspace; Simple and Variant need the W8A8 row scales only.
+size_t workspace_for(Path p, bool w8a8, int x_dtype, size_t m, uint32_t in_dim) {
+  if (p == Path::Gemm && x_dtype == CMK_F32)
+    return row_scale_bytes(m) + cmk::gemm_f32_scratch_bytes((uint32_t)m, in_dim, w8a8);
+  if (p == Path::Gemm && w8a8)
+    return row_scale_bytes(m) + cmk::gemm_w8a8_scratch_bytes((uint32_t)m, in_dim);
+  if (!w8a8 || p == Path::Gemv) return 0;
   return row_scale_bytes(m);
 }
 
@@ -186,8 +194,9 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
                : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, nullptr, nullptr, nullptr);
   // The simple path can still be chosen at launch for unaligned weights; report
   // the larger need so either choice is covered.
-  size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, m, dims.in_dim);
-  size_t need_simple = workspace_for(Path::Simple, md == CMK_ACT_QUANT_W8A8, m, dims.in_dim);
+  size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, (int)x_dtype, m, dims.in_dim);
+  size_t need_simple =
+      workspace_for(Path::Simple, md == CMK_ACT_QUANT_W8A8, (int)x_dtype, m, dims.in_dim);
   *bytes = need > need_simple ? need : need_simple;
   return ok();
 }
@@ -231,7 +240,7 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   Path p = variant != CMK_IQ2_XXS ? Path::Variant
                                   : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x,
                                                 weight_bytes, weight_scales);
-  const size_t need_ws = workspace_for(p, w8a8, m, dims.in_dim);
+  const size_t need_ws = workspace_for(p, w8a8, (int)x_dtype, m, dims.in_dim);
   if (need_ws > 0 && (workspace == nullptr || workspace_bytes < need_ws))
     return fail(CMK_ERR_INVALID_ARGUMENT,
                 "iq2_matmul workspace too small: got %zu expected at least %zu (see "
@@ -248,7 +257,8 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   hipError_t e = hipSuccess;
   float* row_inv = need_ws > 0 ? static_cast<float*>(workspace) : nullptr;
   if (row_inv) {
-    e = cmk::launch_iq2xxs_row_inv_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s);
+    e = w8a8 ? cmk::launch_iq2xxs_row_inv_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s)
+             : cmk::launch_iq2xxs_row_pow2_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s);
     if (e != hipSuccess) return hip_fail(e, "iq2_matmul row scale launch");
   }
   switch (p) {
@@ -259,7 +269,8 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
     case Path::Gemm:
       e = cmk::launch_iq2xxs_gemm(
           x, (int)x_dtype, dims.m, weight_bytes, weight_scales, out, dims.out_dim, dims.in_dim,
-          row_inv, row_inv ? static_cast<uint8_t*>(workspace) + row_scale_bytes(m) : nullptr, s);
+          row_inv, row_inv ? static_cast<uint8_t*>(workspace) + row_scale_bytes(m) : nullptr, w8a8,
+          s);
       break;
     case Path::Simple:
       e = cmk::launch_iq2xxs_matmul_simple(x, (int)x_dtype, dims.m, weight_bytes, weight_scales,

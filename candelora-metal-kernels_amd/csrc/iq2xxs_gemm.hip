@@ -191,7 +191,10 @@ __device__ __forceinline__ void build_gemm_tables(uint32_t tid) {
   for (uint32_t k = 0; k < 16; ++k) gemm_lds_store(base + 16 * ((k + tid) & 15), v);
 }
 
-template <bool kBf16, int BM, int BN, bool kQ>
+// kQ: 0 = plain output; 1 = output row r divided by row_inv[r]; 2 = staged
+// row pairs (2r: the f16 head of x_r * row_inv[r], 2r + 1: the f16 of what
+// the head leaves), output row r = (C[2r] + C[2r+1]) / row_inv[r].
+template <bool kBf16, int BM, int BN, int kQ>
 __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   using L = GemmLayout<BM, BN>;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -464,21 +467,24 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   // the producers' barriers of the padding stages
   for (uint32_t e = a.nk; e < a.nk_pad; ++e) __syncthreads();
 
-  // Epilogue: C[m][n], lane holds rows 4*(lane/16)+r, column lane%16 of each tile.
+  // Epilogue: C[m][n], lane holds rows 4*(lane/16)+r, column lane%16 of each tile
+  // (so a staged pair 2r, 2r + 1 sits in one lane).
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < 4; r += (kQ == 2 ? 2 : 1)) {
       const uint32_t row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-      if (row >= a.m) continue;
-      const float scale = kQ ? a.row_inv[row] : 1.0f;
+      if (row >= a.m) continue;  // a.m is even for kQ == 2: row + 1 is in range too
+      const uint32_t orow = kQ == 2 ? row >> 1 : row;
+      const float scale = kQ ? a.row_inv[orow] : 1.0f;
 #pragma unroll
       for (int jn = 0; jn < NT; ++jn) {
         const uint32_t col = n0 + wn * L::TN + jn * 16 + (lane & 15);
         if (col < a.out_dim) {
           float v = acc[i][jn][r];
-          if constexpr (kQ) v = v / scale;
-          a.out[(size_t)row * a.out_dim + col] = v;
+          if constexpr (kQ == 2) v += acc[i][jn][r + 1];
+          if constexpr (kQ != 0) v = v / scale;
+          a.out[(size_t)orow * a.out_dim + col] = v;
         }
       }
     }
@@ -514,6 +520,49 @@ __global__ __launch_bounds__(256) void iq2xxs_quantize_rows_kernel(const uint16_
   }
 }
 
+// f32 staging pre-pass, eight activations per thread, v = x * row_inv[r]:
+//  kW8A8: q = clamp(round_half_away(v), -127, 127) to staged row r (exact in f16);
+//  else (row_inv a power of two, v exact): the f16 head h = rne(v) to staged
+//  row 2r and the f16 tail rne(v - h) to row 2r + 1 (v - h is exact in fp32),
+//  so the pair carries v to about 2^-22 of its size.
+template <bool kW8A8>
+__global__ __launch_bounds__(256) void iq2xxs_stage_f32_rows_kernel(const float* x, uint32_t m,
+                                                                    uint32_t in_dim,
+                                                                    const float* row_inv,
+                                                                    uint16_t* q) {
+  const uint32_t chunks_per_row = in_dim / 8;
+  const uint64_t total = (uint64_t)m * chunks_per_row;
+  for (uint64_t c = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total;
+       c += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t row = (uint32_t)(c / chunks_per_row);
+    const float inv = row_inv[row];
+    const float4 lo = *reinterpret_cast<const float4*>(x + c * 8);
+    const float4 hi = *reinterpret_cast<const float4*>(x + c * 8 + 4);
+    const float v[8] = {lo.x * inv, lo.y * inv, lo.z * inv, lo.w * inv,
+                        hi.x * inv, hi.y * inv, hi.z * inv, hi.w * inv};
+    if constexpr (kW8A8) {
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        o[k] = pack2<false>(fminf(fmaxf(roundf(v[2 * k]), -127.0f), 127.0f),
+                            fminf(fmaxf(roundf(v[2 * k + 1]), -127.0f), 127.0f));
+      *reinterpret_cast<u32x4*>(q + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
+    } else {
+      uint32_t oh[4], ot[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float h0 = (float)(_Float16)v[2 * k], h1 = (float)(_Float16)v[2 * k + 1];
+        oh[k] = pack2<false>(h0, h1);
+        ot[k] = pack2<false>(v[2 * k] - h0, v[2 * k + 1] - h1);
+      }
+      // chunk c of row r sits at element (2r) * in_dim + (c - r * chunks_per_row) * 8
+      const uint64_t head = c * 8 + (uint64_t)row * in_dim;
+      *reinterpret_cast<u32x4*>(q + head) = u32x4{oh[0], oh[1], oh[2], oh[3]};
+      *reinterpret_cast<u32x4*>(q + head + in_dim) = u32x4{ot[0], ot[1], ot[2], ot[3]};
+    }
+  }
+}
+
 // The activations are loaded in 16-byte chunks that are wholly in or out of
 // range (in_dim % 8 == 0), and every buffer offset stays below
 // kGemmOutOfRange.
@@ -524,7 +573,11 @@ bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim) {
 
 size_t gemm_w8a8_scratch_bytes(uint32_t m, uint32_t in_dim) { return (size_t)m * in_dim * 2; }
 
-template <bool kBf16, int BM, int BN, bool kQ>
+size_t gemm_f32_scratch_bytes(uint32_t m, uint32_t in_dim, bool w8a8) {
+  return (w8a8 ? 1 : 2) * (size_t)m * in_dim * 2;
+}
+
+template <bool kBf16, int BM, int BN, int kQ>
 static hipError_t launch_gemm_t(const GemmArgs& a, hipStream_t stream) {
   using L = GemmLayout<BM, BN>;
   static std::atomic<bool> attr_set{false};
@@ -541,7 +594,7 @@ static hipError_t launch_gemm_t(const GemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <bool kBf16, bool kQ>
+template <bool kBf16, int kQ>
 static hipError_t launch_gemm_shape(const GemmArgs& a, hipStream_t stream) {
   // 256 x 112 tiles halve the dequantisation per CU; used when they still
   // give most CUs a tile.
@@ -552,9 +605,25 @@ static hipError_t launch_gemm_shape(const GemmArgs& a, hipStream_t stream) {
 
 hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              const float* row_inv, void* xq, hipStream_t stream) {
+                              const float* row_inv, void* xq, bool w8a8, hipStream_t stream) {
   const bool bf = x_dtype == 2;
-  if (row_inv) {
+  if (x_dtype == 0) {
+    if (!row_inv || !xq) return hipErrorInvalidValue;
+    const uint64_t chunks = (uint64_t)m * (in_dim / 8);
+    const uint32_t blocks = (uint32_t)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192);
+    if (w8a8)
+      hipLaunchKernelGGL(iq2xxs_stage_f32_rows_kernel<true>, dim3(blocks), dim3(256), 0, stream,
+                         static_cast<const float*>(x), m, in_dim, row_inv,
+                         static_cast<uint16_t*>(xq));
+    else
+      hipLaunchKernelGGL(iq2xxs_stage_f32_rows_kernel<false>, dim3(blocks), dim3(256), 0, stream,
+                         static_cast<const float*>(x), m, in_dim, row_inv,
+                         static_cast<uint16_t*>(xq));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    x = xq;
+    if (!w8a8) m *= 2;  // the staged head / tail rows
+  } else if (row_inv) {
     const uint64_t chunks = (uint64_t)m * (in_dim / 8);
     const uint32_t blocks = (uint32_t)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192);
     if (bf)
@@ -584,8 +653,9 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
   a.x_records = m * in_dim * 2;
   a.wb_records = out_dim * a.bpr * kBytesPerBlock;
   a.ws_records = out_dim * a.bpr * kScalesPerBlock;
-  if (row_inv) return bf ? launch_gemm_shape<true, true>(a, stream) : launch_gemm_shape<false, true>(a, stream);
-  return bf ? launch_gemm_shape<true, false>(a, stream) : launch_gemm_shape<false, false>(a, stream);
+  if (x_dtype == 0 && !w8a8) return launch_gemm_shape<false, 2>(a, stream);
+  if (row_inv) return bf ? launch_gemm_shape<true, 1>(a, stream) : launch_gemm_shape<false, 1>(a, stream);
+  return bf ? launch_gemm_shape<true, 0>(a, stream) : launch_gemm_shape<false, 0>(a, stream);
 }
 
 }  // namespace cmk

@@ -27,6 +27,11 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
 hipError_t launch_iq2xxs_row_inv_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
                                        float* inv_out, hipStream_t stream);
 
+// Power-of-two per-row scale for staging f32 rows as f16: inv[r] =
+// 2^(14 - floor(log2 max|x_r|)), capped at 2^126; 1 for a zero or non-finite max.
+hipError_t launch_iq2xxs_row_pow2_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
+                                        float* inv_out, hipStream_t stream);
+
 // Portable matmul for any alignment / shape (one wave per output row).
 // row_inv: W8A8 per-row scales (from launch_iq2xxs_row_inv_scale) or null.
 hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
@@ -35,16 +40,26 @@ hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, c
                                        hipStream_t stream);
 
 // Prefill matmul (MFMA GEMM, weights dequantised into LDS as f16/bf16);
-// x_dtype must be 1 (f16) or 2 (bf16), on shapes where gemm_supported() holds
+// x_dtype 0 (f32), 1 (f16) or 2 (bf16), on shapes where gemm_supported() holds
 // (in_dim % 8 == 0, x and weights below 2 GB).  Needs 16-byte aligned x and
 // weight_bytes and 2-byte aligned weight_scales.
-// W8A8 (row_inv non-null) first writes the quantised activations to xq, which
-// holds gemm_w8a8_scratch_bytes(m, in_dim) bytes, 16-byte aligned.
+// With row_inv non-null the activations are first written to xq (16-byte
+// aligned) from v = x * row_inv[r], and each output row is divided by
+// row_inv[r]:
+//  - w8a8: q = clamp(round_half_away(v), +-127) in x's half type (exact), inv
+//    from launch_iq2xxs_row_inv_scale; xq holds gemm_w8a8_scratch_bytes (f16 /
+//    bf16 x) or gemm_f32_scratch_bytes(m, in_dim, true) (f32 x);
+//  - f32 x without w8a8: inv from launch_iq2xxs_row_pow2_scale (v exact); row r
+//    is staged as the f16 head rne(v) and tail rne(v - head), two GEMM rows whose
+//    products are summed in the epilogue; xq holds gemm_f32_scratch_bytes(m,
+//    in_dim, false), and gemm_supported must hold for 2m rows.
+// f32 x always needs row_inv and xq.
 bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim);
 size_t gemm_w8a8_scratch_bytes(uint32_t m, uint32_t in_dim);
+size_t gemm_f32_scratch_bytes(uint32_t m, uint32_t in_dim, bool w8a8);
 hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              const float* row_inv, void* xq, hipStream_t stream);
+                              const float* row_inv, void* xq, bool w8a8, hipStream_t stream);
 
 // IQ2_XS (1), IQ2_S (2), IQ3_S (3): bytes / scales per 256-weight block
 // (0 for any other variant), and the portable matmul (any m, any alignment;

@@ -153,6 +153,17 @@ def test_workspace_and_path_queries(cabi):
     assert cabi.matmul_path(cabi.CMK_BF16, 17, 14336, 4096) == "gemm"
     assert cabi.matmul_path(cabi.CMK_F16, 16, 14336, 4096) == "gemv"
     assert cabi.matmul_path(cabi.CMK_F32, 1, 14336, 4096) == "gemv"
+    # f32 rows beyond the GEMV's 16 are staged for the GEMM: row scales plus
+    # f16 head / tail row pairs (mode Off) or the f16 W8A8 rows
+    assert cabi.matmul_path(cabi.CMK_F32, 16, 14336, 4096) == "gemv"
+    assert cabi.matmul_path(cabi.CMK_F32, 17, 14336, 4096) == "gemm"
+    assert cabi.workspace_size(cabi.CMK_F32, 16, 14336, 4096) == 0
+    assert cabi.workspace_size(cabi.CMK_F32, 128, 8192, 8192) == 512 + 2 * 128 * 8192 * 2
+    assert (cabi.workspace_size(cabi.CMK_F32, 64, 4096, 4096, mode=cabi.CMK_ACT_QUANT_W8A8)
+            == 256 + 64 * 4096 * 2)
+    # in_dim % 8 != 0 keeps f32 rows off the GEMM (portable path, no workspace)
+    assert cabi.matmul_path(cabi.CMK_F32, 64, 300, 1001) == "gemv"
+    assert cabi.workspace_size(cabi.CMK_F32, 64, 300, 1001) == 0
     with pytest.raises(cabi.CmkError):
         cabi.workspace_size(cabi.CMK_F16, 1, 0, 4096)
 

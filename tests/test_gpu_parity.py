@@ -300,3 +300,51 @@ def test_gemm_w8a8_bf16_ragged(pkg, oracle, inputs, dev):
     y64 = xq @ w.T
     cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+
+
+# ------------------------------------------------- f32 rows on the GEMM (m > 16)
+
+def f16_weights(oracle, wb, ws, out_dim, in_dim):
+    return oracle.dequantize_f16_bits(wb, ws, out_dim, in_dim).view(np.float16).astype(np.float64)
+
+
+@pytest.mark.parametrize("m,out_dim,in_dim", [(17, 64, 320), (128, 1024, 8192), (300, 230, 1000)])
+def test_gemm_f32_rows_staged(pkg, oracle, inputs, dev, m, out_dim, in_dim):
+    """f32 x beyond the GEMV's rows: v = x * 2^e per row (e brings the row's
+    largest magnitude into [2^14, 2^15)) is staged as an f16 head rne(v) and an
+    f16 tail rne(v - head), two GEMM rows whose products the epilogue sums and
+    divides by 2^e.  The pair carries x to about 2^-22, so against the fp64
+    product of the unrounded x with the f16-dequantised W (what the MFMA GEMM
+    multiplies) the error stays at the fp32-accumulation level: cond <= 1e-5,
+    rel <= 1e-3 (a single f16 rounding of x reads rel 1.4e-2 at 128x1024x8192)."""
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    x = inputs.synthetic_x(m, in_dim)
+    # rows far outside f16's range both ways, and an all-zero row
+    x[0] *= 1e6
+    x[1] *= 1e-9
+    x[2] = 0.0
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim) == "gemm"
+    y = pkg.iq2_matmul(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    w = f16_weights(oracle, wb, ws, out_dim, in_dim)
+    x64 = x.astype(np.float64)
+    y64 = x64 @ w.T
+    assert np.all(y[2] == 0.0)
+    for rows in (slice(0, 1), slice(1, 2), slice(3, m)):  # each row band against its own scale
+        cond, rel = errors(y[rows], y64[rows], np.abs(x64[rows]) @ np.abs(w).T)
+        assert cond <= 1e-5 and rel <= 1e-3, (rows, cond, rel)
+
+
+def test_gemm_f32_rows_w8a8(pkg, oracle, inputs, dev):
+    m, out_dim, in_dim = 64, 256, 1024
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    x = inputs.synthetic_x(m, in_dim) * 3
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev),
+                                             out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                             cfg).cpu().numpy()
+    xq = oracle.rowwise_qdq_w8a8(x, m, in_dim).astype(np.float64)
+    w = f16_weights(oracle, wb, ws, out_dim, in_dim)
+    y64 = xq @ w.T
+    cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
+    assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
