@@ -103,15 +103,25 @@ size_t row_scale_bytes(size_t m) {
   return ((m * sizeof(float) + kWorkspaceAlign - 1) / kWorkspaceAlign) * kWorkspaceAlign;
 }
 
-// The GEMM stages f32 rows (as head / tail pairs) and W8A8 rows in the
-// workspace; Simple and Variant need the W8A8 row scales only.
-size_t workspace_for(Path p, bool w8a8, int x_dtype, size_t m, uint32_t in_dim) {
+// Row scales and staged rows at the head of the workspace: the GEMM stages
+// f32 rows (as head / tail pairs) and W8A8 rows; Simple and Variant need the
+// W8A8 row scales only.
+size_t workspace_head(Path p, bool w8a8, int x_dtype, size_t m, uint32_t in_dim) {
   if (p == Path::Gemm && x_dtype == CMK_F32)
     return row_scale_bytes(m) + cmk::gemm_f32_scratch_bytes((uint32_t)m, in_dim, w8a8);
   if (p == Path::Gemm && w8a8)
     return row_scale_bytes(m) + cmk::gemm_w8a8_scratch_bytes((uint32_t)m, in_dim);
   if (!w8a8 || p == Path::Gemv) return 0;
   return row_scale_bytes(m);
+}
+
+// The head, then for a GEMM split over k its partial products.
+size_t workspace_for(Path p, bool w8a8, int x_dtype, size_t m, uint32_t out_dim,
+                     uint32_t in_dim) {
+  const size_t head = workspace_head(p, w8a8, x_dtype, m, in_dim);
+  if (p != Path::Gemm) return head;
+  const size_t rows = x_dtype == CMK_F32 && !w8a8 ? 2 * m : m;
+  return head + cmk::gemm_split_scratch_bytes((uint32_t)rows, (uint32_t)m, out_dim, in_dim);
 }
 
 // Shared validation of cmk_iq2_matmul / cmk_iq2_matmul_workspace_size.
@@ -194,9 +204,10 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
                : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, nullptr, nullptr, nullptr);
   // The simple path can still be chosen at launch for unaligned weights; report
   // the larger need so either choice is covered.
-  size_t need = workspace_for(p, md == CMK_ACT_QUANT_W8A8, (int)x_dtype, m, dims.in_dim);
-  size_t need_simple =
-      workspace_for(Path::Simple, md == CMK_ACT_QUANT_W8A8, (int)x_dtype, m, dims.in_dim);
+  size_t need =
+      workspace_for(p, md == CMK_ACT_QUANT_W8A8, (int)x_dtype, m, dims.out_dim, dims.in_dim);
+  size_t need_simple = workspace_for(Path::Simple, md == CMK_ACT_QUANT_W8A8, (int)x_dtype, m,
+                                     dims.out_dim, dims.in_dim);
   *bytes = need > need_simple ? need : need_simple;
   return ok();
 }
@@ -240,7 +251,8 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   Path p = variant != CMK_IQ2_XXS ? Path::Variant
                                   : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x,
                                                 weight_bytes, weight_scales);
-  const size_t need_ws = workspace_for(p, w8a8, (int)x_dtype, m, dims.in_dim);
+  const size_t need_ws = workspace_for(p, w8a8, (int)x_dtype, m, dims.out_dim, dims.in_dim);
+  const size_t head_ws = workspace_head(p, w8a8, (int)x_dtype, m, dims.in_dim);
   if (need_ws > 0 && (workspace == nullptr || workspace_bytes < need_ws))
     return fail(CMK_ERR_INVALID_ARGUMENT,
                 "iq2_matmul workspace too small: got %zu expected at least %zu (see "
@@ -255,7 +267,10 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   if (rc != CMK_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
-  float* row_inv = need_ws > 0 ? static_cast<float*>(workspace) : nullptr;
+  float* row_inv = head_ws > 0 ? static_cast<float*>(workspace) : nullptr;
+  float* partials =
+      need_ws > head_ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + head_ws)
+                        : nullptr;
   if (row_inv) {
     e = w8a8 ? cmk::launch_iq2xxs_row_inv_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s)
              : cmk::launch_iq2xxs_row_pow2_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s);
@@ -270,7 +285,7 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
       e = cmk::launch_iq2xxs_gemm(
           x, (int)x_dtype, dims.m, weight_bytes, weight_scales, out, dims.out_dim, dims.in_dim,
           row_inv, row_inv ? static_cast<uint8_t*>(workspace) + row_scale_bytes(m) : nullptr, w8a8,
-          s);
+          partials, s);
       break;
     case Path::Simple:
       e = cmk::launch_iq2xxs_matmul_simple(x, (int)x_dtype, dims.m, weight_bytes, weight_scales,

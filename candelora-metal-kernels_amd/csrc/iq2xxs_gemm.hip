@@ -53,6 +53,7 @@
 // with one xor.
 //
 // Bound: MFMA (arithmetic intensity ~1200 flop/B at m = 512).
+#include <algorithm>
 #include <atomic>
 
 #include "iq2xxs_device.h"
@@ -141,6 +142,10 @@ struct GemmArgs {
   uint32_t nk;      // ceil(in_dim / 32) stages
   uint32_t nk_pad;  // 1 + (nk - 1) rounded up to whole producer loop trips
   uint32_t x_records, wb_records, ws_records;
+  // Split over k (grid z): workgroup z covers blocks [z, z + 1) * split_blocks
+  // of each row and writes its partial products at out + z * out_split.
+  uint32_t split_blocks;
+  uint64_t out_split;
 };
 
 // Barrier of the main loop without a memory fence: waits until at most kVm of
@@ -204,6 +209,8 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t m0 = blockIdx.y * BM;
   const uint32_t n0 = blockIdx.x * BN;
+  const uint32_t blk0 = blockIdx.z * a.split_blocks;  // first block of this k split
+  const uint32_t k0 = blk0 * kQK;
 
   build_gemm_tables(tid);
 
@@ -217,7 +224,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     const bool row_ok = n0 + r < a.out_dim;
     const __amdgpu_buffer_rsrc_t rw = gemm_rsrc(a.wb, a.wb_records);
     const __amdgpu_buffer_rsrc_t rs = gemm_rsrc(a.ws, a.ws_records);
-    const uint32_t row_blk = (n0 + r) * a.bpr;
+    const uint32_t row_blk = (n0 + r) * a.bpr + blk0;
     const uint32_t cs = 16 * (lane & 15);  // selector-table copy of this lane
     const uint32_t css = 16 * (lane & (kGemmSignCopies - 1));  // sign-table copy
     const uint32_t wdst0 = L::kB + r * 64 + 16 * ((2 * h + 0) ^ ((r >> 1) & 3));
@@ -296,10 +303,10 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     for (int k = 0; k < L::kDma; ++k) {
       const uint32_t row = 16 * (L::kDma * pw + k) + (lane >> 2);
       xok[k] = m0 + row < a.m;
-      xsrc[k] = ((m0 + row) * a.in_dim + 8 * xkc) * 2;
+      xsrc[k] = ((m0 + row) * a.in_dim + k0 + 8 * xkc) * 2;
     }
     auto dma_x = [&](uint32_t s) {
-      const bool col_ok = kGemmBK * s + 8 * xkc < a.in_dim;
+      const bool col_ok = k0 + kGemmBK * s + 8 * xkc < a.in_dim;
       const uint32_t abuf = s & 3;
 #pragma unroll
       for (int k = 0; k < L::kDma; ++k) {
@@ -469,6 +476,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
 
   // Epilogue: C[m][n], lane holds rows 4*(lane/16)+r, column lane%16 of each tile
   // (so a staged pair 2r, 2r + 1 sits in one lane).
+  float* const out = a.out + (size_t)blockIdx.z * a.out_split;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -484,7 +492,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
           float v = acc[i][jn][r];
           if constexpr (kQ == 2) v += acc[i][jn][r + 1];
           if constexpr (kQ != 0) v = v / scale;
-          a.out[(size_t)orow * a.out_dim + col] = v;
+          out[(size_t)orow * a.out_dim + col] = v;
         }
       }
     }
@@ -577,8 +585,48 @@ size_t gemm_f32_scratch_bytes(uint32_t m, uint32_t in_dim, bool w8a8) {
   return (w8a8 ? 1 : 2) * (size_t)m * in_dim * 2;
 }
 
+// Sum of the k-split partials in split order (deterministic).
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ part,
+                                                                uint32_t splits, uint64_t n,
+                                                                float* __restrict__ out) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    float v = part[i];
+    for (uint32_t z = 1; z < splits; ++z) v += part[z * n + i];
+    out[i] = v;
+  }
+}
+
+// Tile shape and k split of one launch.  256 x 112 tiles halve the
+// dequantisation per CU and are used when they still give most CUs a tile;
+// when the tiles cannot fill half of the 256 CUs, k is split (at least two
+// blocks per split) until they do.
+struct GemmPlan {
+  bool wide;  // 256 x 112 tiles (else 128 x 128)
+  uint32_t splits, split_blocks;
+};
+
+static GemmPlan plan_gemm(uint32_t rows, uint32_t out_dim, uint32_t in_dim) {
+  GemmPlan p;
+  const uint32_t bpr = (in_dim + kQK - 1) / kQK;
+  const uint64_t t256 = (uint64_t)((rows + 255) / 256) * ((out_dim + 111) / 112);
+  p.wide = t256 >= 192;
+  const uint64_t tiles = p.wide ? t256 : (uint64_t)((rows + 127) / 128) * ((out_dim + 127) / 128);
+  uint64_t splits = 1;
+  if (tiles <= 128 && bpr >= 4) splits = std::min<uint64_t>(256 / tiles, bpr / 2);
+  p.split_blocks = (uint32_t)((bpr + splits - 1) / splits);
+  p.splits = (bpr + p.split_blocks - 1) / p.split_blocks;
+  return p;
+}
+
+size_t gemm_split_scratch_bytes(uint32_t rows, uint32_t out_rows, uint32_t out_dim,
+                                uint32_t in_dim) {
+  const GemmPlan p = plan_gemm(rows, out_dim, in_dim);
+  return p.splits > 1 ? (size_t)p.splits * out_rows * out_dim * sizeof(float) : 0;
+}
+
 template <bool kBf16, int BM, int BN, int kQ>
-static hipError_t launch_gemm_t(const GemmArgs& a, hipStream_t stream) {
+static hipError_t launch_gemm_t(const GemmArgs& a, uint32_t splits, hipStream_t stream) {
   using L = GemmLayout<BM, BN>;
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
@@ -588,25 +636,45 @@ static hipError_t launch_gemm_t(const GemmArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
-  dim3 grid((a.out_dim + BN - 1) / BN, (a.m + BM - 1) / BM);
+  dim3 grid((a.out_dim + BN - 1) / BN, (a.m + BM - 1) / BM, splits);
   hipLaunchKernelGGL((iq2xxs_gemm_kernel<kBf16, BM, BN, kQ>), grid, dim3(kGemmThreads),
                      L::kTotal, stream, a);
   return hipGetLastError();
 }
 
+// out_rows: rows of the output (a.m / 2 for staged pairs).  With a k split
+// the workgroups write partials (the caller's buffer of
+// gemm_split_scratch_bytes) that a second kernel sums into out.
 template <bool kBf16, int kQ>
-static hipError_t launch_gemm_shape(const GemmArgs& a, hipStream_t stream) {
-  // 256 x 112 tiles halve the dequantisation per CU; used when they still
-  // give most CUs a tile.
-  const uint64_t t256 = (uint64_t)((a.m + 255) / 256) * ((a.out_dim + 111) / 112);
-  if (t256 >= 192) return launch_gemm_t<kBf16, 256, 112, kQ>(a, stream);
-  return launch_gemm_t<kBf16, 128, 128, kQ>(a, stream);
+static hipError_t launch_gemm_shape(GemmArgs a, uint32_t out_rows, float* partials,
+                                    hipStream_t stream) {
+  const GemmPlan p = plan_gemm(a.m, a.out_dim, a.in_dim);
+  float* const out = a.out;
+  const uint64_t n = (uint64_t)out_rows * a.out_dim;
+  if (p.splits > 1) {
+    if (!partials) return hipErrorInvalidValue;
+    a.split_blocks = p.split_blocks;
+    a.nk = p.split_blocks * (kQK / kGemmBK);
+    a.nk_pad = 1 + (a.nk - 1 + kGemmUnroll - 1) / kGemmUnroll * kGemmUnroll;
+    a.out = partials;
+    a.out_split = n;
+  }
+  const hipError_t e = p.wide ? launch_gemm_t<kBf16, 256, 112, kQ>(a, p.splits, stream)
+                              : launch_gemm_t<kBf16, 128, 128, kQ>(a, p.splits, stream);
+  if (e != hipSuccess || p.splits == 1) return e;
+  const uint64_t want = (n + 255) / 256;
+  const uint32_t blocks = (uint32_t)(want < 4096 ? want : 4096);
+  hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partials,
+                     p.splits, n, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              const float* row_inv, void* xq, bool w8a8, hipStream_t stream) {
+                              const float* row_inv, void* xq, bool w8a8, float* partials,
+                              hipStream_t stream) {
   const bool bf = x_dtype == 2;
+  const uint32_t out_rows = m;
   if (x_dtype == 0) {
     if (!row_inv || !xq) return hipErrorInvalidValue;
     const uint64_t chunks = (uint64_t)m * (in_dim / 8);
@@ -653,9 +721,14 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
   a.x_records = m * in_dim * 2;
   a.wb_records = out_dim * a.bpr * kBytesPerBlock;
   a.ws_records = out_dim * a.bpr * kScalesPerBlock;
-  if (x_dtype == 0 && !w8a8) return launch_gemm_shape<false, 2>(a, stream);
-  if (row_inv) return bf ? launch_gemm_shape<true, 1>(a, stream) : launch_gemm_shape<false, 1>(a, stream);
-  return bf ? launch_gemm_shape<true, 0>(a, stream) : launch_gemm_shape<false, 0>(a, stream);
+  a.split_blocks = 0;
+  a.out_split = 0;
+  if (x_dtype == 0 && !w8a8) return launch_gemm_shape<false, 2>(a, out_rows, partials, stream);
+  if (row_inv)
+    return bf ? launch_gemm_shape<true, 1>(a, out_rows, partials, stream)
+              : launch_gemm_shape<false, 1>(a, out_rows, partials, stream);
+  return bf ? launch_gemm_shape<true, 0>(a, out_rows, partials, stream)
+            : launch_gemm_shape<false, 0>(a, out_rows, partials, stream);
 }
 
 }  // namespace cmk

@@ -57,9 +57,16 @@ hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, c
 bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim);
 size_t gemm_w8a8_scratch_bytes(uint32_t m, uint32_t in_dim);
 size_t gemm_f32_scratch_bytes(uint32_t m, uint32_t in_dim, bool w8a8);
+// Shapes whose tiles cannot fill the GPU split k over grid z; the launch then
+// writes partial products to `partials` (this many bytes, 16-byte aligned; 0 =
+// no split, partials may be null) and sums them into out in split order.
+// rows: GEMM rows (2m for staged f32 pairs), out_rows: rows of out (m).
+size_t gemm_split_scratch_bytes(uint32_t rows, uint32_t out_rows, uint32_t out_dim,
+                                uint32_t in_dim);
 hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              const float* row_inv, void* xq, bool w8a8, hipStream_t stream);
+                              const float* row_inv, void* xq, bool w8a8, float* partials,
+                              hipStream_t stream);
 
 // IQ2_XS (1), IQ2_S (2), IQ3_S (3): bytes / scales per 256-weight block
 // (0 for any other variant), and the portable matmul (any m, any alignment;

@@ -158,9 +158,17 @@ def test_workspace_and_path_queries(cabi):
     assert cabi.matmul_path(cabi.CMK_F32, 16, 14336, 4096) == "gemv"
     assert cabi.matmul_path(cabi.CMK_F32, 17, 14336, 4096) == "gemm"
     assert cabi.workspace_size(cabi.CMK_F32, 16, 14336, 4096) == 0
-    assert cabi.workspace_size(cabi.CMK_F32, 128, 8192, 8192) == 512 + 2 * 128 * 8192 * 2
+    # (+ the k-split partials where the tiles cannot fill half of the 256 CUs:
+    # 256 staged rows x 8192 -> 128 tiles of 128 x 128, k split in 2)
+    assert (cabi.workspace_size(cabi.CMK_F32, 128, 8192, 8192)
+            == 512 + 2 * 128 * 8192 * 2 + 2 * 128 * 8192 * 4)
+    # 64 rows x 4096 -> 32 tiles, 16 blocks per row split in 8 (two blocks each)
     assert (cabi.workspace_size(cabi.CMK_F32, 64, 4096, 4096, mode=cabi.CMK_ACT_QUANT_W8A8)
-            == 256 + 64 * 4096 * 2)
+            == 256 + 64 * 4096 * 2 + 8 * 64 * 4096 * 4)
+    # half x: partials only; 8 tiles of 128 x 1024, 32 blocks per row split in 16
+    assert cabi.workspace_size(cabi.CMK_F16, 128, 1024, 8192) == 16 * 128 * 1024 * 4
+    # 256 tiles (the M=512 prefill shape) or too few blocks: no split
+    assert cabi.workspace_size(cabi.CMK_BF16, 17, 64, 320) == 0
     # in_dim % 8 != 0 keeps f32 rows off the GEMM (portable path, no workspace)
     assert cabi.matmul_path(cabi.CMK_F32, 64, 300, 1001) == "gemv"
     assert cabi.workspace_size(cabi.CMK_F32, 64, 300, 1001) == 0

@@ -348,3 +348,20 @@ def test_gemm_f32_rows_w8a8(pkg, oracle, inputs, dev):
     y64 = xq @ w.T
     cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+
+
+def test_gemm_k_split_deterministic(pkg, oracle, inputs, dev):
+    """Eight tiles (m=128, out_dim=1024) split k=8192 in 16: the partials are
+    summed in split order, so repeated launches agree bit for bit."""
+    m, out_dim, in_dim = 128, 1024, 8192
+    assert pkg.cabi.workspace_size(pkg.cabi.CMK_F16, m, out_dim, in_dim) > 0
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim), torch.float16, dev)
+    wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
+    a = pkg.iq2_matmul(xt, wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs)
+    b = pkg.iq2_matmul(xt, wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs)
+    assert torch.equal(a, b)
+    w = f16_weights(oracle, wb, ws, out_dim, in_dim)
+    x64 = x_as_f32(xt).astype(np.float64)
+    cond, rel = errors(a.cpu().numpy(), x64 @ w.T, np.abs(x64) @ np.abs(w).T)
+    assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
