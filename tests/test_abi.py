@@ -159,9 +159,9 @@ def test_workspace_and_path_queries(cabi):
     assert cabi.matmul_path(cabi.CMK_F32, 17, 14336, 4096) == "gemm"
     assert cabi.workspace_size(cabi.CMK_F32, 16, 14336, 4096) == 0
     # (+ the k-split partials where the tiles cannot fill half of the 256 CUs:
-    # 256 staged rows x 8192 -> 128 tiles of 128 x 128, k split in 2)
+    # 256 staged rows x 8192 -> 74 tiles of 256 x 112, k split in 3 (11 blocks each))
     assert (cabi.workspace_size(cabi.CMK_F32, 128, 8192, 8192)
-            == 512 + 2 * 128 * 8192 * 2 + 2 * 128 * 8192 * 4)
+            == 512 + 2 * 128 * 8192 * 2 + 3 * 128 * 8192 * 4)
     # 64 rows x 4096 -> 32 tiles, 16 blocks per row split in 8 (two blocks each)
     assert (cabi.workspace_size(cabi.CMK_F32, 64, 4096, 4096, mode=cabi.CMK_ACT_QUANT_W8A8)
             == 256 + 64 * 4096 * 2 + 8 * 64 * 4096 * 4)
