@@ -43,8 +43,11 @@ int hip_fail(hipError_t e, const char* what) {
 size_t bytes_per_block(int v) { return v == CMK_IQ2_XXS ? 64 : cmk::variant_bytes_per_block(v); }
 size_t scales_per_block(int v) { return v == CMK_IQ2_XXS ? 2 : cmk::variant_scales_per_block(v); }
 
-// Largest m served by the GEMV family when x is f16/bf16 (above it: MFMA GEMM).
-constexpr size_t kGemvMaxM = 16;
+// Largest m served by the GEMV family (above it: MFMA GEMM, f32 rows staged).
+// The GEMV re-decodes its tiles for every row (about 3.7 us per row at
+// N=14336); at m=16 the GEMM takes 19 / 30 us against 31 / 58 us
+// (N=4096 / 14336), at m=8 the two are level.
+constexpr size_t kGemvMaxM = 8;
 constexpr size_t kWorkspaceAlign = 256;
 
 bool checked_mul(size_t a, size_t b, size_t* out) {

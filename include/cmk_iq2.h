@@ -93,7 +93,7 @@ typedef enum cmk_act_quant_mode {
  * (:237-259) and x must hold at least m*in_dim elements.
  * Dimensions must be non-zero and fit in u32 (:210-212, :305-311).
  * `workspace` may be NULL when cmk_iq2_matmul_workspace_size reports 0.  The
- * MFMA GEMM (m > 16, in_dim % 8 == 0) needs one for W8A8, for f32 x (each row
+ * MFMA GEMM (m > 8, in_dim % 8 == 0) needs one for W8A8, for f32 x (each row
  * scaled by a power of two and staged as an f16 head / tail pair, so x keeps
  * about 22 bits) and for shapes too small to fill the GPU, whose k is split
  * (partials summed in a fixed order: results are the same on every run).

@@ -137,7 +137,6 @@ GEMV_CASES = [
     (1, 4096, 14336),    # config 1 down
     (4, 4096, 4096),     # config 2
     (8, 1024, 4096),
-    (16, 512, 4096),
     (3, 13, 300),        # ragged N, partial block
     (1, 6, 41),          # K < one sub-block
     (2, 1028, 28672),    # config 4 down-proj K
@@ -302,13 +301,14 @@ def test_gemm_w8a8_bf16_ragged(pkg, oracle, inputs, dev):
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
 
 
-# ------------------------------------------------- f32 rows on the GEMM (m > 16)
+# -------------------------------------------------- f32 rows on the GEMM (m > 8)
 
 def f16_weights(oracle, wb, ws, out_dim, in_dim):
     return oracle.dequantize_f16_bits(wb, ws, out_dim, in_dim).view(np.float16).astype(np.float64)
 
 
-@pytest.mark.parametrize("m,out_dim,in_dim", [(17, 64, 320), (128, 1024, 8192), (300, 230, 1000)])
+@pytest.mark.parametrize("m,out_dim,in_dim", [(9, 4096, 4096), (16, 14336, 4096), (17, 64, 320),
+                                               (128, 1024, 8192), (300, 230, 1000)])
 def test_gemm_f32_rows_staged(pkg, oracle, inputs, dev, m, out_dim, in_dim):
     """f32 x beyond the GEMV's rows: v = x * 2^e per row (e brings the row's
     largest magnitude into [2^14, 2^15)) is staged as an f16 head rne(v) and an
