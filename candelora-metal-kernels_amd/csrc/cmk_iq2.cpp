@@ -274,9 +274,8 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   float* partials =
       need_ws > head_ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + head_ws)
                         : nullptr;
-  if (row_inv) {
-    e = w8a8 ? cmk::launch_iq2xxs_row_inv_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s)
-             : cmk::launch_iq2xxs_row_pow2_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s);
+  if (row_inv && w8a8) {  // (f32 rows staged for the GEMM get their scales there)
+    e = cmk::launch_iq2xxs_row_inv_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s);
     if (e != hipSuccess) return hip_fail(e, "iq2_matmul row scale launch");
   }
   switch (p) {

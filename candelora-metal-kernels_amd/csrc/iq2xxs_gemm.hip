@@ -528,13 +528,9 @@ __global__ __launch_bounds__(256) void iq2xxs_quantize_rows_kernel(const uint16_
   }
 }
 
-// f32 staging pre-pass, eight activations per thread, v = x * row_inv[r]:
-//  kW8A8: q = clamp(round_half_away(v), -127, 127) to staged row r (exact in f16);
-//  else (row_inv a power of two, v exact): the f16 head h = rne(v) to staged
-//  row 2r and the f16 tail rne(v - h) to row 2r + 1 (v - h is exact in fp32),
-//  so the pair carries v to about 2^-22 of its size.
-template <bool kW8A8>
-__global__ __launch_bounds__(256) void iq2xxs_stage_f32_rows_kernel(const float* x, uint32_t m,
+// f32 W8A8 staging pre-pass, eight activations per thread: q = clamp(
+// round_half_away(x * row_inv[r]), -127, 127) to staged row r (exact in f16).
+__global__ __launch_bounds__(256) void iq2xxs_stage_f32_w8a8_kernel(const float* x, uint32_t m,
                                                                     uint32_t in_dim,
                                                                     const float* row_inv,
                                                                     uint16_t* q) {
@@ -542,32 +538,65 @@ __global__ __launch_bounds__(256) void iq2xxs_stage_f32_rows_kernel(const float*
   const uint64_t total = (uint64_t)m * chunks_per_row;
   for (uint64_t c = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; c < total;
        c += (uint64_t)gridDim.x * blockDim.x) {
-    const uint32_t row = (uint32_t)(c / chunks_per_row);
-    const float inv = row_inv[row];
+    const float inv = row_inv[c / chunks_per_row];
     const float4 lo = *reinterpret_cast<const float4*>(x + c * 8);
     const float4 hi = *reinterpret_cast<const float4*>(x + c * 8 + 4);
     const float v[8] = {lo.x * inv, lo.y * inv, lo.z * inv, lo.w * inv,
                         hi.x * inv, hi.y * inv, hi.z * inv, hi.w * inv};
-    if constexpr (kW8A8) {
-      uint32_t o[4];
+    uint32_t o[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        o[k] = pack2<false>(fminf(fmaxf(roundf(v[2 * k]), -127.0f), 127.0f),
-                            fminf(fmaxf(roundf(v[2 * k + 1]), -127.0f), 127.0f));
-      *reinterpret_cast<u32x4*>(q + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
-    } else {
-      uint32_t oh[4], ot[4];
+    for (int k = 0; k < 4; ++k)
+      o[k] = pack2<false>(fminf(fmaxf(roundf(v[2 * k]), -127.0f), 127.0f),
+                          fminf(fmaxf(roundf(v[2 * k + 1]), -127.0f), 127.0f));
+    *reinterpret_cast<u32x4*>(q + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// f32 staging pass, one workgroup of 256 per row r: the power of two
+// inv = 2^(14 - floor(log2 max|x_r|)) (capped at 2^126; 1 for a zero or
+// non-finite max) brings the row's largest magnitude into [2^14, 2^15), so
+// v = x * inv is exact.  The row is then read again (from L2) and staged as the
+// f16 head h = rne(v) in row 2r and the f16 tail rne(v - h) in row 2r + 1
+// (v - h is exact in fp32): the pair carries v to about 2^-22 of its size.
+__global__ __launch_bounds__(256) void iq2xxs_scale_stage_f32_rows_kernel(const float* x,
+                                                                          uint32_t in_dim,
+                                                                          float* row_inv,
+                                                                          uint16_t* q) {
+  __shared__ float s_red[4];
+  const uint32_t row = blockIdx.x;
+  const float4* r4 = reinterpret_cast<const float4*>(x + (size_t)row * in_dim);
+  float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
+#pragma unroll 4
+  for (uint32_t c = threadIdx.x; c < in_dim / 4; c += 256) {
+    const float4 v = r4[c];
+    m0 = fmaxf(m0, fabsf(v.x));
+    m1 = fmaxf(m1, fabsf(v.y));
+    m2 = fmaxf(m2, fabsf(v.z));
+    m3 = fmaxf(m3, fabsf(v.w));
+  }
+  float mx = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float h0 = (float)(_Float16)v[2 * k], h1 = (float)(_Float16)v[2 * k + 1];
-        oh[k] = pack2<false>(h0, h1);
-        ot[k] = pack2<false>(v[2 * k] - h0, v[2 * k + 1] - h1);
-      }
-      // chunk c of row r sits at element (2r) * in_dim + (c - r * chunks_per_row) * 8
-      const uint64_t head = c * 8 + (uint64_t)row * in_dim;
-      *reinterpret_cast<u32x4*>(q + head) = u32x4{oh[0], oh[1], oh[2], oh[3]};
-      *reinterpret_cast<u32x4*>(q + head + in_dim) = u32x4{ot[0], ot[1], ot[2], ot[3]};
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float inv =
+      (mx > 0.0f && mx <= 3.402823466e38f) ? ldexpf(1.0f, min(14 - ilogbf(mx), 126)) : 1.0f;
+  if (threadIdx.x == 0) row_inv[row] = inv;
+  uint16_t* const head = q + (size_t)(2 * row) * in_dim;
+  for (uint32_t c = threadIdx.x; c < in_dim / 8; c += 256) {
+    const float4 lo = r4[2 * c], hi = r4[2 * c + 1];
+    const float v[8] = {lo.x * inv, lo.y * inv, lo.z * inv, lo.w * inv,
+                        hi.x * inv, hi.y * inv, hi.z * inv, hi.w * inv};
+    uint32_t oh[4], ot[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float h0 = (float)(_Float16)v[2 * k], h1 = (float)(_Float16)v[2 * k + 1];
+      oh[k] = pack2<false>(h0, h1);
+      ot[k] = pack2<false>(v[2 * k] - h0, v[2 * k + 1] - h1);
     }
+    *reinterpret_cast<u32x4*>(head + c * 8) = u32x4{oh[0], oh[1], oh[2], oh[3]};
+    *reinterpret_cast<u32x4*>(head + in_dim + c * 8) = u32x4{ot[0], ot[1], ot[2], ot[3]};
   }
 }
 
@@ -681,12 +710,12 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
     const uint64_t chunks = (uint64_t)m * (in_dim / 8);
     const uint32_t blocks = (uint32_t)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192);
     if (w8a8)
-      hipLaunchKernelGGL(iq2xxs_stage_f32_rows_kernel<true>, dim3(blocks), dim3(256), 0, stream,
+      hipLaunchKernelGGL(iq2xxs_stage_f32_w8a8_kernel, dim3(blocks), dim3(256), 0, stream,
                          static_cast<const float*>(x), m, in_dim, row_inv,
                          static_cast<uint16_t*>(xq));
     else
-      hipLaunchKernelGGL(iq2xxs_stage_f32_rows_kernel<false>, dim3(blocks), dim3(256), 0, stream,
-                         static_cast<const float*>(x), m, in_dim, row_inv,
+      hipLaunchKernelGGL(iq2xxs_scale_stage_f32_rows_kernel, dim3(m), dim3(256), 0, stream,
+                         static_cast<const float*>(x), in_dim, const_cast<float*>(row_inv),
                          static_cast<uint16_t*>(xq));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -27,11 +27,6 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
 hipError_t launch_iq2xxs_row_inv_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
                                        float* inv_out, hipStream_t stream);
 
-// Power-of-two per-row scale for staging f32 rows as f16: inv[r] =
-// 2^(14 - floor(log2 max|x_r|)), capped at 2^126; 1 for a zero or non-finite max.
-hipError_t launch_iq2xxs_row_pow2_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
-                                        float* inv_out, hipStream_t stream);
-
 // Portable matmul for any alignment / shape (one wave per output row).
 // row_inv: W8A8 per-row scales (from launch_iq2xxs_row_inv_scale) or null.
 hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
@@ -49,8 +44,9 @@ hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, c
 //  - w8a8: q = clamp(round_half_away(v), +-127) in x's half type (exact), inv
 //    from launch_iq2xxs_row_inv_scale; xq holds gemm_w8a8_scratch_bytes (f16 /
 //    bf16 x) or gemm_f32_scratch_bytes(m, in_dim, true) (f32 x);
-//  - f32 x without w8a8: inv from launch_iq2xxs_row_pow2_scale (v exact); row r
-//    is staged as the f16 head rne(v) and tail rne(v - head), two GEMM rows whose
+//  - f32 x without w8a8: the launch writes row_inv[r] = 2^(14 - floor(log2
+//    max|x_r|)) itself (v exact); row r is staged as the f16 head rne(v) and
+//    tail rne(v - head), two GEMM rows whose
 //    products are summed in the epilogue; xq holds gemm_f32_scratch_bytes(m,
 //    in_dim, false), and gemm_supported must hold for 2m rows.
 // f32 x always needs row_inv and xq.

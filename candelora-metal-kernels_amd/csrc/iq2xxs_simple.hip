@@ -15,11 +15,7 @@ namespace cmk {
 // the row's sub-blocks with byte loads and accumulate exact fp32 weights with
 // fp32 FMA for up to 4 activation rows at a time.
 // ---------------------------------------------------------------------------
-// kPow2 = false: the W8A8 scale 127 / max|x_row| (1 when max < 1e-8).
-// kPow2 = true: the power of two 2^(14 - floor(log2 max|x_row|)) that brings
-// the row's largest magnitude into [2^14, 2^15), exact to multiply and divide
-// by, for staging f32 rows as f16 (1 for an all-zero or non-finite max).
-template <bool kPow2>
+// W8A8 row scale: 127 / max|x_row| (1 when max < 1e-8).
 __global__ __launch_bounds__(256) void iq2xxs_row_inv_scale_kernel(const void* x, int x_dtype,
                                                                    uint32_t in_dim,
                                                                    float* inv_out) {
@@ -50,11 +46,7 @@ __global__ __launch_bounds__(256) void iq2xxs_row_inv_scale_kernel(const void* x
   __syncthreads();
   if (threadIdx.x == 0) {
     float m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    if constexpr (kPow2)
-      inv_out[blockIdx.x] =
-          (m > 0.0f && m <= 3.402823466e38f) ? ldexpf(1.0f, min(14 - ilogbf(m), 126)) : 1.0f;
-    else
-      inv_out[blockIdx.x] = (m < 1e-8f) ? 1.0f : 127.0f / m;
+    inv_out[blockIdx.x] = (m < 1e-8f) ? 1.0f : 127.0f / m;
   }
 }
 
@@ -115,15 +107,8 @@ __global__ __launch_bounds__(256) void iq2xxs_matmul_simple_kernel(
 
 hipError_t launch_iq2xxs_row_inv_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
                                        float* inv_out, hipStream_t stream) {
-  hipLaunchKernelGGL(iq2xxs_row_inv_scale_kernel<false>, dim3(m), dim3(256), 0, stream, x,
-                     x_dtype, in_dim, inv_out);
-  return hipGetLastError();
-}
-
-hipError_t launch_iq2xxs_row_pow2_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
-                                        float* inv_out, hipStream_t stream) {
-  hipLaunchKernelGGL(iq2xxs_row_inv_scale_kernel<true>, dim3(m), dim3(256), 0, stream, x,
-                     x_dtype, in_dim, inv_out);
+  hipLaunchKernelGGL(iq2xxs_row_inv_scale_kernel, dim3(m), dim3(256), 0, stream, x, x_dtype,
+                     in_dim, inv_out);
   return hipGetLastError();
 }
 
