@@ -558,15 +558,14 @@ __global__ __launch_bounds__(256) void iq2xxs_stage_f32_w8a8_kernel(const float*
 // v = x * inv is exact.  The row is then read again (from L2) and staged as the
 // f16 head h = rne(v) in row 2r and the f16 tail rne(v - h) in row 2r + 1
 // (v - h is exact in fp32): the pair carries v to about 2^-22 of its size.
-__global__ __launch_bounds__(256) void iq2xxs_scale_stage_f32_rows_kernel(const float* x,
-                                                                          uint32_t in_dim,
-                                                                          float* row_inv,
-                                                                          uint16_t* q) {
+__global__ __launch_bounds__(256) void iq2xxs_scale_stage_f32_rows_kernel(
+    const float* __restrict__ x, uint32_t in_dim, float* __restrict__ row_inv,
+    uint16_t* __restrict__ q) {
   __shared__ float s_red[4];
   const uint32_t row = blockIdx.x;
   const float4* r4 = reinterpret_cast<const float4*>(x + (size_t)row * in_dim);
   float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
-#pragma unroll 4
+#pragma unroll 8
   for (uint32_t c = threadIdx.x; c < in_dim / 4; c += 256) {
     const float4 v = r4[c];
     m0 = fmaxf(m0, fabsf(v.x));
@@ -584,6 +583,7 @@ __global__ __launch_bounds__(256) void iq2xxs_scale_stage_f32_rows_kernel(const 
       (mx > 0.0f && mx <= 3.402823466e38f) ? ldexpf(1.0f, min(14 - ilogbf(mx), 126)) : 1.0f;
   if (threadIdx.x == 0) row_inv[row] = inv;
   uint16_t* const head = q + (size_t)(2 * row) * in_dim;
+#pragma unroll 4
   for (uint32_t c = threadIdx.x; c < in_dim / 8; c += 256) {
     const float4 lo = r4[2 * c], hi = r4[2 * c + 1];
     const float v[8] = {lo.x * inv, lo.y * inv, lo.z * inv, lo.w * inv,
