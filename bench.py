@@ -50,6 +50,9 @@ METRIC = "IQ2_XXS matmul GB/s (%HBM peak) at M=1; TFLOP/s (%MFMA peak) at M=512"
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_config1_traffic.json")
 
 DECODE_SHAPES = [("gate", 4096, 14336), ("up", 4096, 14336), ("down", 14336, 4096)]
+# Untimed decode steps replayed right before the timed replay (about 7 ms of
+# work at the current speed), so the timed steps run at steady-state clocks.
+DECODE_WARM_STEPS = 300
 
 
 def load_package():
@@ -70,6 +73,25 @@ def alg_bytes(m, k, n, xbytes=4):
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def replay_timed(torch, cabi, graph, sh, steps, warm_steps):
+    """Milliseconds of one replay of `graph` (holding `steps` steps) on stream sh.
+
+    The timed replay is preceded, with no host synchronisation in between, by
+    untimed replays of the same graph covering at least `warm_steps` steps:
+    after a host synchronisation the GPU idles and its clocks take a few
+    milliseconds to ramp back up, so a short replay timed straight after one
+    would measure the ramp instead of the sustained rate."""
+    pre = max(1, math.ceil(warm_steps / max(1, steps)))
+    start, stop = cabi.Event(), cabi.Event()
+    for _ in range(pre):
+        graph.replay()
+    start.record(sh)
+    graph.replay()
+    stop.record(sh)
+    torch.cuda.synchronize()
+    return start.elapsed_ms(stop)
 
 
 class Matmul:
@@ -149,13 +171,8 @@ def bench_decode(pkg, torch, stream, steps, warmup):
         if not torch.equal(out, e):
             raise RuntimeError(f"graph replay differs from eager launch for {name}")
 
-    start, stop = cabi.Event(), cabi.Event()
     torch.cuda.synchronize()
-    start.record(sh)
-    graph.replay()
-    stop.record(sh)
-    torch.cuda.synchronize()
-    ms = start.elapsed_ms(stop)
+    ms = replay_timed(torch, cabi, graph, sh, steps, DECODE_WARM_STEPS)
     step_bytes = sum(alg_bytes(1, k, n) for _, k, n in DECODE_SHAPES)
     launches = steps * len(DECODE_SHAPES)
     return {
@@ -188,12 +205,7 @@ def bench_prefill(pkg, torch, stream, steps, warmup, m=512, k=4096, n=14336):
             call()
     graph.replay()
     torch.cuda.synchronize()
-    start, stop = cabi.Event(), cabi.Event()
-    start.record(sh)
-    graph.replay()
-    stop.record(sh)
-    torch.cuda.synchronize()
-    ms = start.elapsed_ms(stop)
+    ms = replay_timed(torch, cabi, graph, sh, steps, steps)
     flops = 2.0 * m * n * k
     t = ms / 1e3 / steps
     return {"m": m, "k": k, "n": n, "x_dtype": "f16", "ms_per_matmul": t * 1e3,
@@ -234,12 +246,7 @@ def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
                 calls[i % copies]()
         graph.replay()
         torch.cuda.synchronize()
-        start, stop = cabi.Event(), cabi.Event()
-        start.record(sh)
-        graph.replay()
-        stop.record(sh)
-        torch.cuda.synchronize()
-        us = start.elapsed_ms(stop) * 1e3 / steps
+        us = replay_timed(torch, cabi, graph, sh, steps, steps) * 1e3 / steps
         alg = w_bytes + k * 4 + n * 4
         res[name] = {"k": k, "n": n, "m": 1, "mean_launch_us": us, "alg_bytes_per_launch": alg,
                      "gbs": alg / (us * 1e-6) / 1e9,
@@ -261,12 +268,7 @@ def _timed_graph(torch, cabi, stream, sh, run, steps):
             run(i)
     graph.replay()
     torch.cuda.synchronize()
-    start, stop = cabi.Event(), cabi.Event()
-    start.record(sh)
-    graph.replay()
-    stop.record(sh)
-    torch.cuda.synchronize()
-    return start.elapsed_ms(stop) * 1e3 / steps  # microseconds per step
+    return replay_timed(torch, cabi, graph, sh, steps, 4 * steps) * 1e3 / steps  # us per step
 
 
 def bench_configs(pkg, torch, stream):
@@ -378,12 +380,7 @@ def bench_mlp_step(pkg, torch, stream, steps, k=4096, n=14336):
             run(i)
     graph.replay()
     torch.cuda.synchronize()
-    start, stop = cabi.Event(), cabi.Event()
-    start.record(sh)
-    graph.replay()
-    stop.record(sh)
-    torch.cuda.synchronize()
-    us = start.elapsed_ms(stop) * 1e3 / steps
+    us = replay_timed(torch, cabi, graph, sh, steps, steps) * 1e3 / steps
     step_bytes = sum(alg_bytes(1, kk, nn) for _, kk, nn in DECODE_SHAPES) + n * 12
     log(f"[bench] mlp step (gate, up, swiglu, down): {us:.2f} us per step")
     return {"us_per_step": us, "launches_per_step": 4, "alg_bytes_per_step": step_bytes,
@@ -408,6 +405,8 @@ def bench_gguf_split(pkg, torch, stream, steps, k=4096, n=14336):
     call()
     torch.cuda.synchronize()
     start, stop = cabi.Event(), cabi.Event()
+    for _ in range(steps):  # untimed launches first: steady-state clocks
+        call()
     start.record(sh)
     for _ in range(steps):
         call()
@@ -455,10 +454,54 @@ def cpu_baseline(pkg, seconds):
         "unit": "GB/s",
         "cores": used,
         "kind": "port",
+        "cpu_model": cpu_model(),
+        "nproc": os.cpu_count(),
+        "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
         "sample": (f"{reps} full decode steps (gate+up+down, M=1) in {el:.1f} s with the C "
                    f"oracle, OpenMP over outputs; 1-thread gate projection: "
                    f"{alg_bytes(1, k, n)/t1/1e9:.3f} GB/s"),
+        "configs": cpu_config_samples(oracle, inputs, threads),
     }
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_config_samples(oracle, inputs, threads):
+    """The oracle on bounded samples of BASELINE configs 0, 2, 3 and 4 (same
+    threads): configs 0 and 2 whole, config 3 on 8 of its 512 rows (every row
+    costs the same, so the rate is the full matmul's), config 4 at M=1 on the
+    70B layer's gate projection.  Each figure is in the unit its config is
+    quoted in on the GPU (GB/s at small m, GFLOP/s for the prefill)."""
+    res = {}
+
+    def run(name, m, k, n, rows=None, unit="GB/s"):
+        wb, ws = inputs.synthetic_weights(n, k)
+        mm = rows or m
+        x = inputs.synthetic_x(mm, k)
+        t = time.perf_counter()
+        oracle.matmul_reference_mt(x, mm, n, k, wb, ws, threads=threads)
+        t = time.perf_counter() - t
+        if unit == "GB/s":
+            v = alg_bytes(m, k, n) / t / 1e9
+        else:
+            v = 2.0 * mm * k * n / t / 1e9
+        res[name] = {"m": m, "k": k, "n": n, "rows_run": mm, "seconds": round(t, 3),
+                     "value": v, "unit": unit if unit == "GB/s" else "GFLOP/s"}
+
+    run("config0", 1, 4096, 4096)
+    run("config2_m8", 8, 4096, 14336)
+    run("config3_m512", 512, 4096, 14336, rows=8, unit="GFLOP/s")
+    run("config4_gate_m1", 1, 8192, 28672)
+    return res
 
 
 def main():
@@ -548,6 +591,9 @@ def main():
         "frac_of_hbm_peak": value / HBM_PEAK_GBS,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "traffic_source": ("profiles/gemv_config1_traffic.json: rocprofv3 FETCH_SIZE "
+                                        "+ WRITE_SIZE per gate launch, copy-calibrated; read "
+                                        "from the file, not measured in this run"),
                      "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false> "
                                "(XT = 1 for K=4096, 2 for K=14336)",
                      "mean_launch_us": dec["mean_launch_us"],

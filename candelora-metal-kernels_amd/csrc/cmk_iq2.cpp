@@ -43,11 +43,12 @@ int hip_fail(hipError_t e, const char* what) {
 size_t bytes_per_block(int v) { return v == CMK_IQ2_XXS ? 64 : cmk::variant_bytes_per_block(v); }
 size_t scales_per_block(int v) { return v == CMK_IQ2_XXS ? 2 : cmk::variant_scales_per_block(v); }
 
-// Largest m served by the GEMV family (above it: MFMA GEMM, f32 rows staged).
-// The GEMV re-decodes its tiles for every row (about 3.7 us per row at
-// N=14336); at m=16 the GEMM takes 19 / 30 us against 31 / 58 us
-// (N=4096 / 14336), at m=8 the two are level.
+// Largest m served by the GEMV family (above it: the MFMA GEMM).  The GEMV
+// multiplies exact weights; the GEMM rounds them to f16 / bf16, which costs
+// f32 activations the precision they carry, so f32 x keeps the GEMV up to 16
+// rows.  f16 / bf16 x switch at 8 rows, where the two are level in time.
 constexpr size_t kGemvMaxM = 8;
+constexpr size_t kGemvMaxMF32 = 16;
 constexpr size_t kWorkspaceAlign = 256;
 
 bool checked_mul(size_t a, size_t b, size_t* out) {
@@ -91,7 +92,8 @@ Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, const
   // f32 rows beyond the GEMV's range are staged as scaled f16 head / tail row
   // pairs for the GEMM (twice the rows).
   const size_t gemm_rows = x_dtype == CMK_F32 ? 2 * m : m;
-  if (m > kGemvMaxM && gemm_rows <= UINT32_MAX &&
+  const size_t gemv_max_m = x_dtype == CMK_F32 ? kGemvMaxMF32 : kGemvMaxM;
+  if (m > gemv_max_m && gemm_rows <= UINT32_MAX &&
       cmk::gemm_supported((uint32_t)gemm_rows, out_dim, in_dim) && al(x, 16) && al(wb, 16) &&
       al(ws, 2))
     return Path::Gemm;

@@ -151,6 +151,54 @@ struct XOctet {
   }
 };
 
+// The exact fp32 weight at (row, col), evaluated as the reference does:
+// (d * (0.5 + s) * 0.25) * g, negated under its sign bit
+// (src/iq2_matmul.rs:853-866 with accum_word_grid :789-809;
+// iq2_matmul.metal:8-28,201-232).  Byte loads, any alignment.
+__device__ inline float iq2xxs_weight_at(const uint8_t* wb, const uint8_t* ws, uint32_t row,
+                                         uint32_t col, uint32_t bpr) {
+  const size_t block = (size_t)row * bpr + col / kQK;
+  const uint32_t ib32 = (col % kQK) / 32, g = (col % 32) / 8, j = col % 8;
+  const uint8_t* q = wb + block * kBytesPerBlock + ib32 * 8;
+  const uint32_t aux_s =
+      (uint32_t)q[4] | ((uint32_t)q[5] << 8) | ((uint32_t)q[6] << 16) | ((uint32_t)q[7] << 24);
+  const uint8_t* sp = ws + block * kScalesPerBlock;
+  const float d = half_bits_to_float((uint16_t)(sp[0] | (sp[1] << 8)));
+  const float dl = d * (0.5f + (float)(aux_s >> 28)) * 0.25f;
+  const uint32_t sidx = (aux_s >> (7 * g)) & 127u;
+  const uint32_t sbyte = sidx | ((__popc(sidx) & 1u) << 7);
+  const uint32_t code = ((uint32_t)kGridCodesDev[q[g]] >> (2 * j)) & 3u;
+  const float mag = dl * (code == 0 ? 8.0f : (code == 1 ? 25.0f : 43.0f));
+  return ((sbyte >> j) & 1u) ? -mag : mag;
+}
+
+// Activations that are NaN or infinite.  The digit paths hold x as finite
+// integers, so those values are set aside: they enter the digits as zeros, and
+// the sum over them, x_c * w_rc, is added to each output afterwards.  Every
+// such term is NaN or an infinity, so the sum only depends on which kinds
+// occur, never on their order:
+//   NaN term, or infinities of both signs -> NaN; otherwise the infinity;
+// and a finite partial sum plus that value is what the reference's
+// sequential fp32 loop yields (src/iq2_matmul.rs:789-809).
+constexpr uint32_t kAbsMask = 0x7FFFFFFFu;
+constexpr uint32_t kInfBits = 0x7F800000u;  // |x| bits at or above: not finite
+constexpr uint32_t kSpecialNaN = 1u, kSpecialPosInf = 2u, kSpecialNegInf = 4u;
+
+__device__ __forceinline__ uint32_t special_kind(float t) {
+  return t != t ? kSpecialNaN : (t > 0.0f ? kSpecialPosInf : kSpecialNegInf);
+}
+
+// The sum of the set-aside terms of an output from the kinds that occurred
+// (0 when none did).
+__device__ __forceinline__ float special_value(uint32_t kinds) {
+  if ((kinds & kSpecialNaN) || (kinds & (kSpecialPosInf | kSpecialNegInf)) ==
+                                   (kSpecialPosInf | kSpecialNegInf))
+    return __uint_as_float(0x7FC00000u);
+  if (kinds & kSpecialPosInf) return __uint_as_float(kInfBits);
+  if (kinds & kSpecialNegInf) return -__uint_as_float(kInfBits);
+  return 0.0f;
+}
+
 // W8A8 fake quantisation of one activation (src/metal_src/iq2_matmul.metal:98-102):
 // q = clamp(round_half_away(x * inv), -127, 127); return q / inv.
 __device__ __forceinline__ float qdq_w8a8(float x, float inv_scale) {

@@ -211,6 +211,14 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   const uint32_t n0 = blockIdx.x * BN;
   const uint32_t blk0 = blockIdx.z * a.split_blocks;  // first block of this k split
   const uint32_t k0 = blk0 * kQK;
+  // Stages of this workgroup's k range.  Splits cover split_blocks blocks each
+  // except the last, which ends at the row's end (an uneven split is shorter).
+  uint32_t nk = a.nk, nk_pad = a.nk_pad;
+  if (a.split_blocks) {
+    const uint32_t k_end = min(k0 + a.split_blocks * (uint32_t)kQK, a.in_dim);
+    nk = (k_end - k0 + kGemmBK - 1) / kGemmBK;
+    nk_pad = 1 + (nk - 1 + kGemmUnroll - 1) / kGemmUnroll * kGemmUnroll;
+  }
 
   build_gemm_tables(tid);
 
@@ -230,9 +238,11 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     const uint32_t wdst0 = L::kB + r * 64 + 16 * ((2 * h + 0) ^ ((r >> 1) & 3));
     const uint32_t wdst1 = L::kB + r * 64 + 16 * ((2 * h + 1) ^ ((r >> 1) & 3));
 
-    // Codes of one block (eight stages) and its scale.  Past the row's end
-    // the loads read zeros or the next row: such stages are padding that no
-    // consumer reads.
+    // Codes of one block (eight stages) and its scale.  Stages past nk (the
+    // padding that completes the last loop trip) load codes past this
+    // workgroup's k range -- zeros past the buffer's end, or the blocks that
+    // follow -- and are written to LDS but never read: the consumers stop at
+    // stage nk.
     struct Codes {
       u32x4 q[4];  // sub-blocks 2j, 2j + 1 of the block
       uint32_t d;
@@ -349,7 +359,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     // covers kGemmUnroll steps from s0 = 1 (mod 16), so every set choice and
     // wait count below is a compile-time constant and the body is one
     // straight-line sequence (exact wait counts).
-    for (uint32_t s0 = 1; s0 < a.nk_pad; s0 += kGemmUnroll) {
+    for (uint32_t s0 = 1; s0 < nk_pad; s0 += kGemmUnroll) {
 #pragma unroll
       for (int j = 0; j < kGemmUnroll; ++j) {
         const uint32_t s = s0 + j;
@@ -452,7 +462,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   uint32_t ab = 0;  // activation tile of stage s
   read_frags(ab, 0, f0);
   uint32_t s = 0;
-  for (; s + 2 < a.nk; s += 2) {
+  for (; s + 2 < nk; s += 2) {
     mfma_rows01(f0);
     stage_barrier<0>();
     ab = next_tile(ab);
@@ -465,14 +475,14 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   // the last one or two stages
   mfma_rows(f0, 0);
   mfma_rows(f0, 2);
-  if (s + 1 < a.nk) {
+  if (s + 1 < nk) {
     __syncthreads();
     read_frags(next_tile(ab), s + 1, f1);
     mfma_rows(f1, 0);
     mfma_rows(f1, 2);
   }
   // the producers' barriers of the padding stages
-  for (uint32_t e = a.nk; e < a.nk_pad; ++e) __syncthreads();
+  for (uint32_t e = nk; e < nk_pad; ++e) __syncthreads();
 
   // Epilogue: C[m][n], lane holds rows 4*(lane/16)+r, column lane%16 of each tile
   // (so a staged pair 2r, 2r + 1 sits in one lane).
@@ -553,34 +563,41 @@ __global__ __launch_bounds__(256) void iq2xxs_stage_f32_w8a8_kernel(const float*
 }
 
 // f32 staging pass, one workgroup of 256 per row r: the power of two
-// inv = 2^(14 - floor(log2 max|x_r|)) (capped at 2^126; 1 for a zero or
-// non-finite max) brings the row's largest magnitude into [2^14, 2^15), so
-// v = x * inv is exact.  The row is then read again (from L2) and staged as the
-// f16 head h = rne(v) in row 2r and the f16 tail rne(v - h) in row 2r + 1
-// (v - h is exact in fp32): the pair carries v to about 2^-22 of its size.
+// inv = 2^(14 - floor(log2 max|x_r|)) (capped at 2^126; 1 for a zero max),
+// with the max taken over the row's finite values, brings the row's largest
+// finite magnitude into [2^14, 2^15), so v = x * inv is exact.  The row is
+// then read again (from L2) and staged as the f16 head h = rne(v) in row 2r
+// and the f16 tail rne(v - h) in row 2r + 1 (v - h is exact in fp32): the
+// pair carries v to about 2^-22 of its size.  A NaN or an infinity is staged
+// as itself in the head with a zero tail, so the MFMA products carry it to the
+// output as the reference's fp32 loop would.
 __global__ __launch_bounds__(256) void iq2xxs_scale_stage_f32_rows_kernel(
     const float* __restrict__ x, uint32_t in_dim, float* __restrict__ row_inv,
     uint16_t* __restrict__ q) {
   __shared__ float s_red[4];
   const uint32_t row = blockIdx.x;
   const float4* r4 = reinterpret_cast<const float4*>(x + (size_t)row * in_dim);
-  float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f;
+  // magnitudes as integer bits; NaN and infinities count as 0
+  auto fin = [](float v) {
+    const uint32_t b = __float_as_uint(v) & kAbsMask;
+    return b < kInfBits ? b : 0u;
+  };
+  uint32_t m0 = 0, m1 = 0, m2 = 0, m3 = 0;
 #pragma unroll 8
   for (uint32_t c = threadIdx.x; c < in_dim / 4; c += 256) {
     const float4 v = r4[c];
-    m0 = fmaxf(m0, fabsf(v.x));
-    m1 = fmaxf(m1, fabsf(v.y));
-    m2 = fmaxf(m2, fabsf(v.z));
-    m3 = fmaxf(m3, fabsf(v.w));
+    m0 = max(m0, fin(v.x));
+    m1 = max(m1, fin(v.y));
+    m2 = max(m2, fin(v.z));
+    m3 = max(m3, fin(v.w));
   }
-  float mx = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+  float mx = __uint_as_float(max(max(m0, m1), max(m2, m3)));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  const float inv =
-      (mx > 0.0f && mx <= 3.402823466e38f) ? ldexpf(1.0f, min(14 - ilogbf(mx), 126)) : 1.0f;
+  const float inv = mx > 0.0f ? ldexpf(1.0f, min(14 - ilogbf(mx), 126)) : 1.0f;
   if (threadIdx.x == 0) row_inv[row] = inv;
   uint16_t* const head = q + (size_t)(2 * row) * in_dim;
 #pragma unroll 4
@@ -593,7 +610,8 @@ __global__ __launch_bounds__(256) void iq2xxs_scale_stage_f32_rows_kernel(
     for (int k = 0; k < 4; ++k) {
       const float h0 = (float)(_Float16)v[2 * k], h1 = (float)(_Float16)v[2 * k + 1];
       oh[k] = pack2<false>(h0, h1);
-      ot[k] = pack2<false>(v[2 * k] - h0, v[2 * k + 1] - h1);
+      ot[k] = pack2<false>(fin(v[2 * k]) ? v[2 * k] - h0 : 0.0f,
+                           fin(v[2 * k + 1]) ? v[2 * k + 1] - h1 : 0.0f);
     }
     *reinterpret_cast<u32x4*>(head + c * 8) = u32x4{oh[0], oh[1], oh[2], oh[3]};
     *reinterpret_cast<u32x4*>(head + in_dim + c * 8) = u32x4{ot[0], ot[1], ot[2], ot[3]};

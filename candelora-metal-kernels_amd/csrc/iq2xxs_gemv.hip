@@ -190,11 +190,9 @@ __device__ __forceinline__ float sum_over_blocks(float v) {
 }
 
 // Max over the 4 lanes of an aligned quad (DPP quad_perm [1,0,3,2], [2,3,0,1]).
-__device__ __forceinline__ float quad_max(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF,
-                                                          false)));
-  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF,
-                                                             false)));
+__device__ __forceinline__ uint32_t quad_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
 }
 
 // Eight consecutive activations (one digitisation task) by buffer loads.  An
@@ -255,7 +253,7 @@ struct GemvArgs {
   uint32_t ntasks;        // digitisation tasks per activation row (8 columns each)
   uint32_t wb_records, ws_records, x_records;  // bytes addressable by the buffer loads
   uint32_t plane_stride;  // LDS bytes between the three digit planes
-  uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs;  // LDS layout
+  uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs, flag_ofs;  // LDS layout
   int w8a8;
 };
 
@@ -273,6 +271,10 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   uint8_t* xdig = lds + a.xdig_ofs;
   float* red = reinterpret_cast<float*>(lds + a.red_ofs);
   float* s_wred = reinterpret_cast<float*>(lds + a.wred_ofs);
+  // Generation number of the last digitised row that held a NaN or an
+  // infinity (rows are numbered by `gen` below; 0 = none yet).
+  uint32_t* s_special = reinterpret_cast<uint32_t*>(lds + a.flag_ofs);
+  uint32_t* s_kinds = reinterpret_cast<uint32_t*>(lds + a.red_ofs);
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63;
@@ -373,21 +375,36 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   };
   // Digits of the round of tasks held in xo: 4 threads per 32-column chunk
   // (an aligned quad of lanes), 8 columns each.
-  auto digitize_round = [&](uint32_t r0, float inv_scale) {
+  // The chunk maximum is taken over the magnitude bits as integers, so a NaN
+  // (or an infinity) shows up as a value at or above kInfBits; such a chunk
+  // (rare) has those values set to zero and marks the row for the fix-up in
+  // reduce_and_store.  The condition is the same on the 4 lanes of a quad.
+  auto digitize_round = [&](uint32_t r0, float inv_scale, uint32_t gen) {
 #pragma unroll
     for (uint32_t u = 0; u < (uint32_t)kXT; ++u) {
       const uint32_t task = r0 + u * kGemvThreads + rtid;
       float xv[8];
-      float mx = 0.0f;
+      uint32_t mb = 0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         xv[k] = xo[u].get(k);
         if constexpr (kW8A8) xv[k] = qdq_w8a8(xv[k], inv_scale);
-        mx = fmaxf(mx, fabsf(xv[k]));
+        mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
       }
-      mx = quad_max(mx);
+      mb = quad_max_u32(mb);
+      if (mb >= kInfBits) {
+        mb = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t ab = __float_as_uint(xv[k]) & kAbsMask;
+          if (ab >= kInfBits) xv[k] = 0.0f;
+          mb = max(mb, ab < kInfBits ? ab : 0u);
+        }
+        mb = quad_max_u32(mb);
+        if (task < a.ntasks) *s_special = gen;
+      }
       if (task < a.ntasks) {
-        const int e = digit_exponent(mx);
+        const int e = digit_exponent(__uint_as_float(mb));
         const float scale = ldexpf(1.0f, kDigitShift - e);
         uint32_t dg[8];
 #pragma unroll
@@ -405,14 +422,17 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   };
   // Digits of row mrow whose first round is in xo; rounds beyond the first
   // (in_dim > 8192 * kXT) load behind the first weight tiles.
+  float inv_row = 1.0f;  // W8A8 scale of the digitised row
+  uint32_t gen = 0;      // number of rows digitised so far
   auto digitize_row = [&](uint32_t mrow) {
-    float inv_scale = 1.0f;
-    if constexpr (kW8A8) inv_scale = w8a8_inv_scale(mrow);
-    digitize_round(0, inv_scale);
+    ++gen;
+    inv_row = 1.0f;
+    if constexpr (kW8A8) inv_row = w8a8_inv_scale(mrow);
+    digitize_round(0, inv_row, gen);
     if constexpr (kMulti) {
       for (uint32_t r0 = round; r0 < a.ntasks; r0 += round) {
         load_x(r0, mrow);
-        digitize_round(r0, inv_scale);
+        digitize_round(r0, inv_row, gen);
       }
     }
   };
@@ -513,6 +533,30 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     const float ud1 = (float)((words[3] & 0xF0000000u) | 0x07FFFFFFu) * d;
     return fmaf(f1 * ud1, xs[1], (f0 * ud0) * xs[0]);
   };
+  // Adds the set-aside terms of activation row mrow (NaN or infinite x) to the
+  // chunk's outputs: every thread scans its columns of x; for each such column
+  // it forms x_c * w_rc for the chunk's rows and records the kind of the term.
+  // Only runs for rows that held such a value.
+  auto fix_up_special = [&](uint32_t mrow) {
+    sync();  // the partial sums in red are consumed: red holds the kinds now
+    for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) s_kinds[rl] = 0;
+    sync();
+    const size_t xbase = (size_t)mrow * a.in_dim;
+    for (uint32_t c = tid; c < a.in_dim; c += kGemvThreads) {
+      float v = x_bits_to_float<XD>(load_x_bits<XD>(a.x, xbase + c));
+      if constexpr (kW8A8) v = qdq_w8a8(v, inv_row);
+      if ((__float_as_uint(v) & kAbsMask) < kInfBits) continue;
+      for (uint32_t rl = 0; rl < rows; ++rl)
+        atomicOr(&s_kinds[rl],
+                 special_kind(v * iq2xxs_weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr)));
+    }
+    sync();
+    for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
+      const uint32_t kinds = s_kinds[rl];
+      float* o = a.out + (size_t)mrow * a.out_dim + row_begin + rl;
+      if (kinds) *o = *o + special_value(kinds);
+    }
+  };
   // Row sums of the chunk's tiles for activation row mrow, into out.
   auto reduce_and_store = [&](uint32_t mrow) {
 #pragma unroll
@@ -525,18 +569,21 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       if (lane < 4) red[(rgl * a.nslices + slice) * 4 + j] = v;
     }
     sync();
+    const bool special = *s_special == gen;  // uniform
     for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
       const float* p = red + (rl >> 2) * a.nslices * 4 + (rl & 3);
       float sum = 0.0f;
       for (uint32_t sl = 0; sl < a.nslices; ++sl) sum += p[sl * 4];
       a.out[(size_t)mrow * a.out_dim + row_begin + rl] = sum;
     }
+    if (special) fix_up_special(mrow);
   };
 
   // ======== first chunk, activation row 0 (straight-line) ========
   set_chunk(chunk);
   // 1. set-up loads, ahead of every weight load
   const uint32_t code = tid < 256 ? kGridCodesDev[tid] : 0u;
+  if (tid == 0) *s_special = 0;
   load_scales();
   load_x(0, 0);
   sync();
@@ -615,7 +662,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 // ---------------------------------------------------------------------------
 struct GemvPlan {
   uint32_t nslices, rg_per_chunk, nchunks, grid, ntasks, xt, plane_stride;
-  uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs;
+  uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs, flag_ofs;
   size_t lds;
   bool wide;
 };
@@ -657,7 +704,7 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   p->plane_stride = (uint32_t)(nsb * 32 + 16);
   const uint64_t scale_bytes = align16(rg_per_chunk * 4 * nslices * (kSlicePairs / 4) * 2);
   const uint64_t rest = scale_bytes + align16(nsb * 4) + 3ull * p->plane_stride +
-                        align16(rg_per_chunk * nslices * 16) + kGemvWaves * 4;
+                        align16(rg_per_chunk * nslices * 16) + kGemvWaves * 4 + 16;
   p->wide = GemvTables<true>::kBytes + rest <= kGemvLdsLimit;
   const uint32_t tb = p->wide ? GemvTables<true>::kBytes : GemvTables<false>::kBytes;
   p->scale_ofs = tb;
@@ -665,7 +712,8 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   p->xdig_ofs = p->xsc_ofs + align16(nsb * 4);
   p->red_ofs = p->xdig_ofs + 3 * p->plane_stride;
   p->wred_ofs = p->red_ofs + align16(rg_per_chunk * nslices * 16);
-  p->lds = p->wred_ofs + kGemvWaves * 4;
+  p->flag_ofs = p->wred_ofs + kGemvWaves * 4;
+  p->lds = p->flag_ofs + 16;
   return p->lds <= kGemvLdsLimit;
 }
 
@@ -746,6 +794,7 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
   a.xdig_ofs = p.xdig_ofs;
   a.red_ofs = p.red_ofs;
   a.wred_ofs = p.wred_ofs;
+  a.flag_ofs = p.flag_ofs;
   a.w8a8 = w8a8 ? 1 : 0;
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&

@@ -11,6 +11,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <sstream>
 
 #include "cmk_iq2.h"
@@ -317,6 +318,46 @@ void check_sizes(const char* op, const Tensor& weight_bytes, const Tensor& weigh
          std::to_string(expected_scales));
 }
 
+// Device scratch of cmk_iq2_matmul, one buffer per device, kept between calls
+// and replaced by a larger one only when a call needs more (freeing the old one
+// waits for the device).  Every launch of this layer goes to the device's
+// default stream, which runs them in order, so calls never overlap on the
+// buffer; the mutex is held from the lookup until the launch is enqueued, so
+// no thread replaces a buffer another thread is about to pass.  A steady
+// stream of calls therefore neither allocates nor synchronises.
+class WorkspaceCache {
+ public:
+  static constexpr int kMaxDevices = 64;
+  std::mutex mu;
+
+  // Caller holds mu.
+  void* get(int ordinal, size_t bytes) {
+    if (ordinal < 0 || ordinal >= kMaxDevices) bail("device ordinal out of range");
+    Slot& s = slots_[ordinal];
+    if (s.bytes < bytes) {
+      check_abi(cmk_set_device(ordinal));
+      if (s.ptr) check_abi(cmk_free(s.ptr));
+      s.ptr = nullptr;
+      s.bytes = 0;
+      check_abi(cmk_malloc(&s.ptr, bytes));
+      s.bytes = bytes;
+    }
+    return s.ptr;
+  }
+
+ private:
+  struct Slot {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+  };
+  Slot slots_[kMaxDevices];
+};
+
+WorkspaceCache& workspace_cache() {
+  static WorkspaceCache* cache = new WorkspaceCache();  // lives until the process ends
+  return *cache;
+}
+
 // The ROCm body of iq2_matmul_metal (src/iq2_matmul.rs:197-365), checks in the
 // reference's order.
 Tensor iq2_matmul_hip(const Tensor& x, const Tensor& weight_bytes, const Tensor& weight_scales,
@@ -357,16 +398,16 @@ Tensor iq2_matmul_hip(const Tensor& x, const Tensor& weight_bytes, const Tensor&
       mode == ActivationQuantMode::W8A8 ? CMK_ACT_QUANT_W8A8 : CMK_ACT_QUANT_OFF;
   size_t ws_bytes = 0;
   check_abi(cmk_iq2_matmul_workspace_size(xd, m, out_dim, in_dim, to_abi(variant), am, &ws_bytes));
-  Tensor work;
-  if (ws_bytes) work = Tensor::empty({ws_bytes}, DType::U8, x.device());
+  WorkspaceCache& cache = workspace_cache();
+  std::lock_guard<std::mutex> lk(cache.mu);
+  void* work = ws_bytes ? cache.get(x.device().ordinal, ws_bytes) : nullptr;
+  check_abi(cmk_set_device(x.device().ordinal));
   check_abi(cmk_iq2_matmul(x2.data_ptr(), xd, x2.elem_count(), m,
                            static_cast<const uint8_t*>(weight_bytes.data_ptr()),
                            weight_bytes.elem_count(),
                            static_cast<const uint8_t*>(weight_scales.data_ptr()),
                            weight_scales.elem_count(), out_dim, in_dim, to_abi(variant), am, 0,
-                           static_cast<float*>(out.data_ptr_mut()),
-                           ws_bytes ? work.data_ptr_mut() : nullptr, ws_bytes, nullptr));
-  if (ws_bytes) synchronize();  // `work` is freed when it goes out of scope
+                           static_cast<float*>(out.data_ptr_mut()), work, ws_bytes, nullptr));
   return squeeze ? out.squeeze(0) : out;
 }
 

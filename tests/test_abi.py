@@ -153,12 +153,14 @@ def test_workspace_and_path_queries(cabi):
     assert cabi.matmul_path(cabi.CMK_BF16, 9, 14336, 4096) == "gemm"
     assert cabi.matmul_path(cabi.CMK_F16, 8, 14336, 4096) == "gemv"
     assert cabi.matmul_path(cabi.CMK_F32, 1, 14336, 4096) == "gemv"
-    # f32 rows beyond the GEMV's 8 are staged for the GEMM: row scales plus
-    # f16 head / tail row pairs (mode Off) or the f16 W8A8 rows
+    # f32 rows keep the exact-weight GEMV up to 16 rows; beyond, they are
+    # staged for the GEMM: row scales plus f16 head / tail row pairs (mode Off)
+    # or the f16 W8A8 rows
     assert cabi.matmul_path(cabi.CMK_F32, 8, 14336, 4096) == "gemv"
-    assert cabi.matmul_path(cabi.CMK_F32, 9, 14336, 4096) == "gemm"
-    assert cabi.matmul_path(cabi.CMK_F32, 16, 14336, 4096) == "gemm"
-    assert cabi.workspace_size(cabi.CMK_F32, 8, 14336, 4096) == 0
+    assert cabi.matmul_path(cabi.CMK_F32, 9, 14336, 4096) == "gemv"
+    assert cabi.matmul_path(cabi.CMK_F32, 16, 14336, 4096) == "gemv"
+    assert cabi.matmul_path(cabi.CMK_F32, 17, 14336, 4096) == "gemm"
+    assert cabi.workspace_size(cabi.CMK_F32, 16, 14336, 4096) == 0
     # (+ the k-split partials where the tiles cannot fill half of the 256 CUs:
     # 256 staged rows x 8192 -> 74 tiles of 256 x 112, k split in 3 (11 blocks each))
     assert (cabi.workspace_size(cabi.CMK_F32, 128, 8192, 8192)

@@ -1,0 +1,160 @@
+"""GPU parity at the edges: non-finite activations, uneven k splits of the MFMA
+GEMM, and the Llama-3-70B layer's projections at M=128.
+
+Non-finite x.  The reference's loop (src/iq2_matmul.rs:789-809,
+iq2_matmul.metal:8-28) adds x_c * w_rc in fp32, so one NaN activation makes
+every output of its row NaN, an infinity makes an output +-inf (NaN where its
+weight is 0, i.e. d = 0, or where infinities of both signs meet).  The tests
+compare the class of every output (finite / +inf / -inf / NaN) with the oracle's
+exactly, and the finite outputs with the usual bars.
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+from test_gpu_parity import errors, f16_weights, to_dev, x_as_f32, x_tensor  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def dev(pkg):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    pkg.cabi.lib()  # fail loudly when the HIP library is missing
+    return torch.device("cuda:0")
+
+
+def classes(y):
+    """0 finite, 1 +inf, 2 -inf, 3 NaN."""
+    y = np.asarray(y)
+    return np.where(np.isnan(y), 3, np.where(np.isposinf(y), 1, np.where(np.isneginf(y), 2, 0)))
+
+
+# Non-finite patterns: (column, value) pairs written into row 0 of x.
+NONFINITE = {
+    "nan": [(100, np.nan)],
+    "posinf": [(2049, np.inf)],
+    "neginf": [(7, -np.inf)],
+    "both_inf": [(300, np.inf), (3000, -np.inf)],
+    "inf_and_nan": [(5, np.inf), (4095, np.nan)],
+}
+
+
+def _weights_with_zero_d(inputs, out_dim, in_dim, zero_rows, block):
+    """Seeded weights with d = 0 in `block` of the given rows (their weights
+    in that block are 0, so an infinite x there gives inf * 0 = NaN)."""
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    ws = ws.copy()
+    bpr = (in_dim + 255) // 256
+    for r in zero_rows:
+        ws[2 * (r * bpr + block)] = 0
+        ws[2 * (r * bpr + block) + 1] = 0
+    return wb, ws
+
+
+@pytest.mark.parametrize("pattern", sorted(NONFINITE))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,out_dim,in_dim", [(1, 14336, 4096), (1, 4096, 14336), (2, 1024, 4096)])
+def test_gemv_nonfinite_x(pkg, oracle, inputs, dev, pattern, dtype, m, out_dim, in_dim):
+    """Config-1 shapes (gate/up and down) and a two-row case on the GEMV."""
+    zero_rows = [3, 17, out_dim - 1]
+    cols = [c for c, _ in NONFINITE[pattern]]
+    wb, ws = _weights_with_zero_d(inputs, out_dim, in_dim, zero_rows, cols[0] // 256)
+    x = inputs.synthetic_x(m, in_dim)
+    for c, v in NONFINITE[pattern]:
+        x[0, c % in_dim] = v
+    xt = x_tensor(x, dtype, dev)
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim) == "gemv"
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    xf = x_as_f32(xt)
+    ref, _ = oracle.matmul_reference_mt(xf, m, out_dim, in_dim, wb, ws)
+    assert np.array_equal(classes(y), classes(ref)), pattern
+    if pattern in ("posinf", "neginf"):  # the d = 0 rows meet inf * 0
+        assert np.all(np.isnan(y[0, zero_rows]))
+    fin = classes(ref) == 0
+    if fin.any():
+        y64, sc = oracle.matmul_f64(np.where(np.isfinite(xf), xf, 0.0), m, out_dim, in_dim, wb, ws)
+        cond, rel = errors(y[fin], y64[fin], sc[fin])
+        assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+
+
+@pytest.mark.parametrize("pattern", ["nan", "posinf", "both_inf"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_gemm_nonfinite_x(pkg, oracle, inputs, dev, pattern, dtype):
+    """The MFMA GEMM (f32 rows staged, f16 / bf16 x as given): a NaN or an
+    infinity in row 0 of x reaches row 0 of the output as in the reference;
+    the other rows stay finite."""
+    m, out_dim, in_dim = 40, 512, 4096
+    zero_rows = [3, 17]
+    cols = [c for c, _ in NONFINITE[pattern]]
+    wb, ws = _weights_with_zero_d(inputs, out_dim, in_dim, zero_rows, cols[0] // 256)
+    x = inputs.synthetic_x(m, in_dim)
+    for c, v in NONFINITE[pattern]:
+        x[0, c] = v
+    xt = x_tensor(x, dtype, dev)
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim) == "gemm"
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    ref, _ = oracle.matmul_reference_mt(x_as_f32(xt), m, out_dim, in_dim, wb, ws)
+    assert np.array_equal(classes(y), classes(ref)), pattern
+    assert np.all(np.isfinite(y[1:]))
+
+
+def test_gemm_uneven_k_split_stops_at_row_end(pkg, oracle, inputs, dev):
+    """64 rows x 1024 columns give 8 tiles of 128 x 128, so k = 1792 (7 blocks)
+    is split 3 + 3 + 1.  The last split must stop after its one block: weight
+    row r + 1 starts right after row r's last block, and a NaN scale there must
+    not reach output column r."""
+    m, out_dim, in_dim = 64, 1024, 1792
+    bpr = 7
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    ws = ws.copy()
+    nan_row = 101
+    for blk in range(bpr):  # every block of row nan_row has a NaN scale
+        ws[2 * (nan_row * bpr + blk)] = 0x00
+        ws[2 * (nan_row * bpr + blk) + 1] = 0x7E
+    assert pkg.cabi.workspace_size(pkg.cabi.CMK_F16, m, out_dim, in_dim) == 3 * m * out_dim * 4
+    xt = x_tensor(inputs.synthetic_x(m, in_dim), torch.float16, dev)
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    assert np.all(np.isnan(y[:, nan_row]))
+    others = np.ones(out_dim, bool)
+    others[nan_row] = False
+    assert np.all(np.isfinite(y[:, others]))
+    w = f16_weights(oracle, wb, ws, out_dim, in_dim)[others]
+    x64 = x_as_f32(xt).astype(np.float64)
+    cond, rel = errors(y[:, others], x64 @ w.T, np.abs(x64) @ np.abs(w).T)
+    assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+
+
+# BASELINE config 4 at M=128: q / o (8192 x 8192), gate / up (K=8192, N=28672)
+# and down (K=28672, N=8192); k / v (N=1024) are in test_gpu_parity.
+CONFIG4_M128 = [(8192, 8192), (28672, 8192), (8192, 28672)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("out_dim,in_dim", CONFIG4_M128)
+def test_config4_m128_vs_device_dequant(pkg, inputs, dev, dtype, out_dim, in_dim):
+    """Full-size config-4 projections at M=128 on the MFMA GEMM (with the k
+    split these shapes take): against an fp64 product with the device
+    dequantisation to f16 (bit-exact with the oracle, tested elsewhere)."""
+    m = 128
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim, seed=11)
+    wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim, seed=12), dtype, dev)
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim) == "gemm"
+    y = pkg.iq2_matmul(xt, wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs).double()
+    w = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                  out_dtype=torch.float16).double()
+    x64 = xt.double()
+    y64 = x64 @ w.T
+    sc = x64.abs() @ w.abs().T
+    cond, rel = errors(y.cpu().numpy(), y64.cpu().numpy(), sc.cpu().numpy())
+    # f32 rows are staged as f16 head / tail pairs (x to about 2^-22): the
+    # error is the fp32 accumulation's; f16 x is exact in the MFMA.
+    assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+    del w, x64, y64, sc

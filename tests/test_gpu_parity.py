@@ -135,7 +135,14 @@ GEMV_CASES = [
     (1, 4096, 4096),     # config 0
     (1, 14336, 4096),    # config 1 gate/up
     (1, 4096, 14336),    # config 1 down
-    (4, 4096, 4096),     # config 2
+    (4, 4096, 4096),     # config 2: M in {4, 8, 16} x N in {4096, 14336}, K=4096
+    (4, 14336, 4096),
+    (8, 4096, 4096),
+    (8, 14336, 4096),
+    (16, 4096, 4096),    # (f32 x keeps the exact-weight GEMV up to 16 rows)
+    (16, 14336, 4096),
+    (9, 512, 4096),
+    (16, 512, 4096),
     (8, 1024, 4096),
     (3, 13, 300),        # ragged N, partial block
     (1, 6, 41),          # K < one sub-block
@@ -307,10 +314,10 @@ def f16_weights(oracle, wb, ws, out_dim, in_dim):
     return oracle.dequantize_f16_bits(wb, ws, out_dim, in_dim).view(np.float16).astype(np.float64)
 
 
-@pytest.mark.parametrize("m,out_dim,in_dim", [(9, 4096, 4096), (16, 14336, 4096), (17, 64, 320),
+@pytest.mark.parametrize("m,out_dim,in_dim", [(17, 4096, 4096), (17, 64, 320),
                                                (128, 1024, 8192), (300, 230, 1000)])
 def test_gemm_f32_rows_staged(pkg, oracle, inputs, dev, m, out_dim, in_dim):
-    """f32 x beyond the GEMV's rows: v = x * 2^e per row (e brings the row's
+    """f32 x beyond the GEMV's rows (16): v = x * 2^e per row (e brings the row's
     largest magnitude into [2^14, 2^15)) is staged as an f16 head rne(v) and an
     f16 tail rne(v - head), two GEMM rows whose products the epilogue sums and
     divides by 2^e.  The pair carries x to about 2^-22, so against the fp64
