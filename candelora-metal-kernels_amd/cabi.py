@@ -27,6 +27,7 @@ CMK_ACT_QUANT_OFF, CMK_ACT_QUANT_W8A8, CMK_ACT_QUANT_W4A8 = 0, 1, 2
 # Every symbol include/cmk_iq2.h declares (checked by tests/test_abi.py).
 EXPORTED = (
     "cmk_iq2_matmul",
+    "cmk_iq2_matmul_noalloc",
     "cmk_iq2_matmul_workspace_size",
     "cmk_iq2_dequantize",
     "cmk_iq2_split_gguf_blocks",
@@ -76,6 +77,8 @@ def lib() -> ctypes.CDLL:
     P, S, I = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
     L.cmk_iq2_matmul.argtypes = [P, I, S, S, P, S, P, S, S, S, I, I, I, P, P, S, P]
     L.cmk_iq2_matmul.restype = I
+    L.cmk_iq2_matmul_noalloc.argtypes = [P, I, S, S, P, S, P, S, S, S, I, I, I, P, P]
+    L.cmk_iq2_matmul_noalloc.restype = I
     L.cmk_iq2_matmul_workspace_size.argtypes = [I, S, S, S, I, I, ctypes.POINTER(S)]
     L.cmk_iq2_matmul_workspace_size.restype = I
     L.cmk_iq2_dequantize.argtypes = [P, S, P, S, S, S, I, I, P, P]
@@ -124,6 +127,19 @@ def matmul_raw(x_ptr, x_dtype, x_len, m, wb_ptr, wb_len, ws_ptr, ws_len, out_dim
     check(lib().cmk_iq2_matmul(x_ptr, x_dtype, x_len, m, wb_ptr, wb_len, ws_ptr, ws_len, out_dim,
                                in_dim, variant, mode, 1 if strict else 0, out_ptr, workspace_ptr,
                                workspace_bytes, stream))
+
+
+def matmul_noalloc_raw(x_ptr, x_dtype, x_len, m, wb_ptr, wb_len, ws_ptr, ws_len, out_dim, in_dim,
+                       out_ptr, variant=CMK_IQ2_XXS, mode=CMK_ACT_QUANT_OFF, strict=False,
+                       stream=None) -> None:
+    """cmk_iq2_matmul_noalloc: the library's own per-device scratch instead of a
+    workspace argument (up to NOALLOC_SCRATCH_BYTES)."""
+    check(lib().cmk_iq2_matmul_noalloc(x_ptr, x_dtype, x_len, m, wb_ptr, wb_len, ws_ptr, ws_len,
+                                       out_dim, in_dim, variant, mode, 1 if strict else 0,
+                                       out_ptr, stream))
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # CMK_IQ2_NOALLOC_SCRATCH_BYTES
 
 
 def workspace_size(x_dtype, m, out_dim, in_dim, variant=CMK_IQ2_XXS,

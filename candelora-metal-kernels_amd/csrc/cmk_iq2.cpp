@@ -188,6 +188,41 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Scratch of cmk_iq2_matmul_noalloc: one array per device, part of the code
+// object, so it exists on every device the library runs on until the process
+// ends.  In host code `scratch` only names the symbol; the device address of
+// each device's copy comes from hipGetSymbolAddress, called once per device
+// (with that device current) on the first call there, and is kept below.
+static __device__ __align__(256) uint8_t scratch[CMK_IQ2_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// Device address of the current device's scratch array.
+int device_scratch(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(CMK_ERR_NO_DEVICE, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(CMK_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return CMK_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* cmk_last_error(void) { return g_last_error.c_str(); }
@@ -303,6 +338,37 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   }
   if (e != hipSuccess) return hip_fail(e, "iq2_matmul launch");
   return ok();
+}
+
+int cmk_iq2_matmul_noalloc(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
+                           const uint8_t* weight_bytes, size_t weight_bytes_len,
+                           const uint8_t* weight_scales, size_t weight_scales_len, size_t out_dim,
+                           size_t in_dim, cmk_iq2_variant variant, cmk_act_quant_mode mode,
+                           int strict, float* out, void* stream) {
+  int md = (int)mode;
+  Dims dims;
+  int rc = validate_matmul((int)x_dtype, m, out_dim, in_dim, (int)variant, &md, strict,
+                           weight_bytes_len, weight_scales_len, true, &dims);
+  if (rc != CMK_OK) return rc;
+  if (m == 0) return ok();
+  const Path p = variant != CMK_IQ2_XXS ? Path::Variant
+                                        : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim,
+                                                      x, weight_bytes, weight_scales);
+  const size_t need =
+      workspace_for(p, md == CMK_ACT_QUANT_W8A8, (int)x_dtype, m, dims.out_dim, dims.in_dim);
+  if (need > (size_t)CMK_IQ2_NOALLOC_SCRATCH_BYTES)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "cmk_iq2_matmul_noalloc needs %zu bytes of scratch for these arguments, more "
+                "than its fixed %zu (call cmk_iq2_matmul with a workspace instead)",
+                need, (size_t)CMK_IQ2_NOALLOC_SCRATCH_BYTES);
+  void* work = nullptr;
+  if (need > 0) {
+    rc = device_scratch(&work);
+    if (rc != CMK_OK) return rc;
+  }
+  return cmk_iq2_matmul(x, x_dtype, x_len, m, weight_bytes, weight_bytes_len, weight_scales,
+                        weight_scales_len, out_dim, in_dim, variant, mode, strict, out, work,
+                        need > 0 ? (size_t)CMK_IQ2_NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 int cmk_iq2_dequantize(const uint8_t* weight_bytes, size_t weight_bytes_len,

@@ -105,6 +105,29 @@ int cmk_iq2_matmul(const void *x, cmk_dtype x_dtype, size_t x_len, size_t m,
                    cmk_act_quant_mode mode, int strict,
                    float *out, void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * cmk_iq2_matmul without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * hosts that forbid allocation).  No counterpart in the reference, whose
+ * dispatch allocates its output per call (src/iq2_matmul.rs:261).  Same
+ * arguments, checks, kernels and results as cmk_iq2_matmul; the scratch the
+ * launch needs (the MFMA GEMM's staged rows, row scales and k-split partials)
+ * comes from an array inside the library, one per device, of
+ * CMK_IQ2_NOALLOC_SCRATCH_BYTES bytes.  Arguments that need more fail with
+ * CMK_ERR_INVALID_ARGUMENT before anything is launched.  The call performs no
+ * device allocation: the array is part of the code object and lives until the
+ * process ends; the first call on a device looks up its address once.  All
+ * calls on one device share that device's array and nothing clears it between
+ * calls (every launch writes what it reads): calls that can overlap on one
+ * device -- different streams, or host threads without ordering -- race on it.
+ */
+#define CMK_IQ2_NOALLOC_SCRATCH_BYTES (32u << 20)
+int cmk_iq2_matmul_noalloc(const void *x, cmk_dtype x_dtype, size_t x_len, size_t m,
+                           const uint8_t *weight_bytes, size_t weight_bytes_len,
+                           const uint8_t *weight_scales, size_t weight_scales_len,
+                           size_t out_dim, size_t in_dim, cmk_iq2_variant variant,
+                           cmk_act_quant_mode mode, int strict, float *out, void *stream);
+
 /* Device scratch (bytes) that cmk_iq2_matmul needs for these arguments.  The
  * launch never allocates; callers that get a non-zero size pass a buffer of at
  * least that many bytes.  Same argument validation as cmk_iq2_matmul. */
