@@ -232,10 +232,16 @@ __device__ __forceinline__ int digit_exponent(float max_abs) {
   return e < -100 ? -100 : e;
 }
 
+// The three digit bytes of x (bits 0..23) each plus 128, for chunk scale
+// 2^(20-e): the bytes of v + 0x808080.
+__device__ __forceinline__ uint32_t digitize_biased(float x, float scale) {
+  const uint32_t bits = __float_as_uint(fmaf(x, scale, kDigitMagic));
+  return bits - kDigitBias;
+}
+
 // Three signed digit bytes (bits 0..23) of x for chunk exponent e.
 __device__ __forceinline__ uint32_t digitize(float x, float scale) {
-  const uint32_t bits = __float_as_uint(fmaf(x, scale, kDigitMagic));
-  return (bits - kDigitBias) ^ 0x808080u;
+  return digitize_biased(x, scale) ^ 0x808080u;
 }
 
 // Transpose the digit bytes of 4 values into one dword per plane.

@@ -72,7 +72,7 @@ constexpr uint32_t kGemvWaves = 16;
 constexpr uint32_t kGemvThreads = kGemvWaves * 64;
 constexpr uint32_t kSlicePairs = 16;   // sub-block pairs per tile (one per 4x4 block)
 constexpr uint32_t kTilesPerWave = 4;  // weight tiles a wave holds
-constexpr uint32_t kTilesAhead = 2;    // tiles in flight ahead of the one computed
+constexpr uint32_t kTilesEarly = 2;    // tiles issued before the set-up work
 constexpr uint32_t kScaleLoads = 2;    // staged scales per thread and chunk
 constexpr uint32_t kGemvLdsLimit = 160 * 1024;
 // Buffer offset past every num_records used here (buffers are < 2^31 bytes).
@@ -84,17 +84,25 @@ constexpr int kStreamLoad = 2;
 
 // Table layouts at LDS offset 0.
 //  wide:   [0, 64K)   codebook row e (256 B) = 16 copies of {g lo, g hi, -g lo, -g hi}
-//          [64K, 96K) sign row i (256 B) = 32 copies of the 8-byte mask of ksigns(i)
+//          [64K, 80K) sign row i (128 B) = 16 copies of the 8-byte mask of ksigns(i);
+//          the 128-byte stride puts the index of sign field g (bits 7g..7g+6
+//          of aux_s) at address bits 7..13 with one shift and one v_and_or
+//          (field 1 needs no shift)
 //  narrow: [0, 64K)   row r (256 B): bytes [0,128) 8 codebook copies of entry r,
 //          bytes [128, 256) 16 copies of the sign mask of ksigns(r & 127); the
 //          sign index then needs no masking (a byte of aux_s << g carries one
 //          unrelated bit on top), at the price of 2-way bank conflicts.
+// Lane l reads copy l & 15 of a row, so the 16 lanes the LDS serves together
+// hit 16 different bank groups (measured on gfx950 with 16 waves: about 3.0
+// clocks per wave-wide 16-byte read with 16 copies against 4.9 with 8, and
+// 2.6 per 8-byte read with 16 copies against 2.4 with 32).
 template <bool kWide>
 struct GemvTables {
-  static constexpr uint32_t kBytes = kWide ? 96 * 1024 : 64 * 1024;
+  static constexpr uint32_t kBytes = kWide ? 80 * 1024 : 64 * 1024;
   static constexpr uint32_t kGridCopies = kWide ? 16 : 8;
-  static constexpr uint32_t kSignCopies = kWide ? 32 : 16;
+  static constexpr uint32_t kSignCopies = 16;
   static constexpr uint32_t kSignBase = kWide ? 65536 : 128;
+  static constexpr uint32_t kSignStride = kWide ? 128 : 256;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
@@ -102,29 +110,55 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uin
                                            kBufferWord3);
 }
 
-// All copies of codebook row e; the copy order is rotated by e so the 16
-// lanes the LDS serves together write 16 different bank groups.
+// Four level codes (2 bits each, x4 = bits 0..7) as four magnitude bytes
+// {8, 25, 43}: the codes are spread to one per byte with two multiplies
+// (fields 0 and 2, and fields 1 and 3, land in disjoint bits), then select
+// from the byte pool {8, 25, 43, 0} with one v_perm.
+__device__ __forceinline__ uint32_t level_bytes(uint32_t x4) {
+  const uint32_t even = ((x4 & 0x33u) * 0x1001u) & 0x00030003u;   // codes 0, 2 -> bytes 0, 2
+  const uint32_t odd = ((x4 & 0xCCu) * 0x40040u) & 0x03000300u;   // codes 1, 3 -> bytes 1, 3
+  return __builtin_amdgcn_perm(0u, 0x002B1908u, even | odd);
+}
+
+// Bit j of the nibble n as byte j of the result: 0xFF where set.  The nibble's
+// copies at shifts 0, 7, 14, 21 do not overlap, so the multiply places bit j at
+// bit 8j without carries.
+__device__ __forceinline__ uint32_t byte_mask4(uint32_t n) {
+  const uint32_t t = (n * 0x00204081u) & 0x01010101u;
+  return (t << 8) - t;
+}
+
+// All copies of codebook row e (code c: 2-bit level codes of its 8 bytes); the
+// copy order is rotated by e so the 16 lanes the LDS serves together write 16
+// different bank groups.
 template <bool kWide>
-__device__ __forceinline__ void store_grid_row(uint8_t* lds, uint32_t e, uint64_t g) {
-  const uint32_t lo = (uint32_t)g, hi = (uint32_t)(g >> 32);
+__device__ __forceinline__ void store_grid_row(uint8_t* lds, uint32_t e, uint32_t c) {
+  const uint32_t lo = level_bytes(c & 0xFFu), hi = level_bytes(c >> 8);
   // per-byte negation: (~g) + 1 never carries across bytes since g >= 8
   const u32x4 v = {lo, hi, ~lo + 0x01010101u, ~hi + 0x01010101u};
   constexpr uint32_t C = GemvTables<kWide>::kGridCopies;
-#pragma unroll 2
+  const uint32_t row = e * 256, rot = 16 * e;
+#pragma unroll
   for (uint32_t k = 0; k < C; ++k)
-    *reinterpret_cast<u32x4*>(lds + e * 256 + 16 * ((k + e) & (C - 1))) = v;
+    *reinterpret_cast<u32x4*>(lds + (row | ((rot + 16 * k) & (16 * C - 16)))) = v;
+}
+
+// The 8-byte mask of ksigns(i) = i | parity(i) << 7.
+__device__ __forceinline__ u32x2 sign_mask(uint32_t i) {
+  const uint32_t sb = i | ((__popc(i) & 1u) << 7);
+  return u32x2{byte_mask4(sb & 0xFu), byte_mask4(sb >> 4)};
 }
 
 // Copies [k0, k0 + n) of sign row i (rotated like the codebook rows).
 template <bool kWide>
-__device__ __forceinline__ void store_sign_row(uint8_t* lds, uint32_t i, uint64_t m, uint32_t k0,
+__device__ __forceinline__ void store_sign_row(uint8_t* lds, uint32_t i, u32x2 v, uint32_t k0,
                                                uint32_t n) {
-  const u32x2 v = {(uint32_t)m, (uint32_t)(m >> 32)};
-  constexpr uint32_t C = GemvTables<kWide>::kSignCopies;
-#pragma unroll 2
+  using TL = GemvTables<kWide>;
+  constexpr uint32_t C = TL::kSignCopies;
+  uint8_t* const row = lds + TL::kSignBase + i * TL::kSignStride;
+#pragma unroll
   for (uint32_t k = k0; k < k0 + n; ++k)
-    *reinterpret_cast<u32x2*>(lds + GemvTables<kWide>::kSignBase + i * 256 +
-                              8 * ((k + i) & (C - 1))) = v;
+    *reinterpret_cast<u32x2*>(row + 8 * ((k + i) & (C - 1))) = v;
 }
 
 // Table address  256 * byte G of w + low byte of cbase  as one v_perm
@@ -134,13 +168,16 @@ __device__ __forceinline__ uint32_t perm_addr(uint32_t w, uint32_t cbase) {
   return __builtin_amdgcn_perm(w, cbase, 0x0C0C0000u | ((0x04u + G) << 8));
 }
 
-// Sign-row address of group G of aux_s for this lane's copy base cs.
+// Sign-row address of group G of aux_s for this lane's copy base cs (whose
+// bits 7..13 are clear).
 template <bool kWide, int G>
 __device__ __forceinline__ uint32_t sign_addr(uint32_t aux_s, uint32_t cs) {
-  if constexpr (kWide)
-    return (__builtin_amdgcn_ubfe(aux_s, 7 * G, 7) << 8) | cs;
-  else
+  if constexpr (kWide) {
+    const uint32_t f = G == 0 ? aux_s << 7 : (G == 1 ? aux_s : aux_s >> (7 * G - 7));
+    return (f & 0x3F80u) | cs;
+  } else {
     return perm_addr<G>(aux_s << G, cs);
+  }
 }
 
 // LDS reads at byte addresses (the kernel's dynamic LDS starts at 0).
@@ -174,19 +211,43 @@ __device__ __forceinline__ void pin_here(u32x4& v) {
   asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 
-// Sum over the 16 lanes that share lane & 3 (the 16 4x4 blocks), in a fixed
-// order, with VALU lane moves only.
+// Sum over the 16 lanes that share lane & 3 (the 16 4x4 blocks) of one
+// tile, with VALU lane moves only: lanes l and l ^ 32, then l and l ^ 16, then
+// the row's four blocks (row_ror:4, row_ror:8).  Every add sees the same
+// operands as in sum_over_blocks4, so a row's result does not depend on which
+// of the two reductions the kernel took (results do not depend on m).
 __device__ __forceinline__ float sum_over_blocks(float v) {
-  // row_ror:4 and row_ror:8 inside each 16-lane row
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
-  // then across rows: lanes l and l ^ 16, then l and l ^ 32
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(s[0]) + __uint_as_float(s[1]);
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                   false);
   v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  return v;
+}
+
+// The sums over the 16 blocks of four tiles at once: afterwards every lane l
+// holds the sum for tile l >> 4 and row l & 3.  v_permlane32_swap swaps the
+// upper 32 lanes of its first operand with the lower 32 lanes of its second,
+// so adding the two results leaves tile a in lanes 0-31 and tile b in lanes
+// 32-63 (each summed over lanes l and l ^ 32); v_permlane16_swap does the same
+// with the odd rows of the first operand and the even rows of the second,
+// leaving tile 0, 1, 2, 3 in rows 0, 1, 2, 3; two row rotations then add the
+// row's four blocks.  Three swaps and five adds for four tiles, in a fixed
+// order.
+__device__ __forceinline__ float sum_over_blocks4(float a0, float a1, float a2, float a3) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a0), __float_as_uint(a2), false,
+                                            false);
+  const float t02 = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a1), __float_as_uint(a3), false, false);
+  const float t13 = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(t02), __float_as_uint(t13), false, false);
+  float v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+  return v;
 }
 
 // Max over the 4 lanes of an aligned quad (DPP quad_perm [1,0,3,2], [2,3,0,1]).
@@ -246,6 +307,7 @@ struct GemvArgs {
   uint32_t bpr;           // super-blocks per row
   uint32_t spr;           // staged scales per row: bpr rounded up to whole slices
   uint32_t spr_magic;     // ceil(2^32 / spr): i / spr = umulhi(i, spr_magic) for i < 2^16
+  int scale_dw;           // spr == bpr and weight_scales 4-byte aligned: dword scale loads
   uint32_t npairs;        // sub-block pairs per row = 4 * bpr
   uint32_t nslices;       // tiles per row group = ceil(npairs / 16)
   uint32_t rg_per_chunk;  // row groups per chunk
@@ -266,6 +328,10 @@ template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti>
 __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   using TL = GemvTables<kWide>;
+  // Tiles in flight ahead of the one computed: three for one chunk and row;
+  // the looping kernels keep two (a third would exceed the 128 VGPRs a wave of
+  // a 1024-thread workgroup has and spill).
+  constexpr uint32_t kTilesAhead = kMulti ? 2 : 3;
   uint16_t* sscale = reinterpret_cast<uint16_t*>(lds + a.scale_ofs);
   float* xsc = reinterpret_cast<float*>(lds + a.xsc_ofs);
   uint8_t* xdig = lds + a.xdig_ofs;
@@ -321,7 +387,22 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // Super-block scales of the chunk, staged as rows of a.spr entries (blocks
   // padded to whole slices) with zeros for padding rows and blocks.
   uint32_t sraw[kScaleLoads];
+  // (the looping kernels keep the 2-byte loads and the one-tile reductions:
+  // they are at the 128-VGPR limit, and the alternatives cost spills)
   auto load_scales = [&]() {
+    if (!kMulti && a.scale_dw) {
+      // a chunk's scales are contiguous and staged as they lie: rows*bpr/2
+      // dwords (rows is a multiple of 4 or the chunk ends the matrix, and bpr is
+      // then even); dwords past them read zeros
+      const uint32_t ndw = (rows * a.bpr + 1) / 2;
+#pragma unroll
+      for (uint32_t k = 0; k < kScaleLoads; ++k) {
+        const uint32_t t = tid + k * kGemvThreads;
+        sraw[k] = __builtin_amdgcn_raw_buffer_load_b32(
+            rs, t < ndw ? row_begin * a.bpr * kScalesPerBlock + 4 * t : kOutOfRange, 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (uint32_t k = 0; k < kScaleLoads; ++k) {
       const uint32_t i = tid + k * kGemvThreads;
@@ -333,6 +414,14 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   };
   auto stage_scales = [&]() {
     const uint32_t nstaged = a.rg_per_chunk * 4 * a.spr;
+    if (!kMulti && a.scale_dw) {
+#pragma unroll
+      for (uint32_t k = 0; k < kScaleLoads; ++k) {
+        const uint32_t t = tid + k * kGemvThreads;
+        if (2 * t < nstaged) reinterpret_cast<uint32_t*>(sscale)[t] = sraw[k];
+      }
+      return;
+    }
 #pragma unroll
     for (uint32_t k = 0; k < kScaleLoads; ++k) {
       const uint32_t i = tid + k * kGemvThreads;
@@ -406,12 +495,20 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       if (task < a.ntasks) {
         const int e = digit_exponent(__uint_as_float(mb));
         const float scale = ldexpf(1.0f, kDigitShift - e);
+        // biased digit bytes (each digit + 128), transposed into planes, then
+        // the bias removed from four digits at a time
         uint32_t dg[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) dg[k] = digitize(xv[k], scale);
+        for (int k = 0; k < 8; ++k) dg[k] = digitize_biased(xv[k], scale);
         uint32_t p0[2], p1[2], p2[2];
         digits_to_planes(dg[0], dg[1], dg[2], dg[3], p0[0], p1[0], p2[0]);
         digits_to_planes(dg[4], dg[5], dg[6], dg[7], p0[1], p1[1], p2[1]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          p0[h] ^= 0x80808080u;
+          p1[h] ^= 0x80808080u;
+          p2[h] ^= 0x80808080u;
+        }
         const uint32_t c0 = (task >> 2) * 32 + (task & 3) * 8;
         *reinterpret_cast<uint2*>(xdig + c0) = make_uint2(p0[0], p0[1]);
         *reinterpret_cast<uint2*>(xdig + a.plane_stride + c0) = make_uint2(p1[0], p1[1]);
@@ -472,6 +569,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       }
     }
   };
+  uint32_t k27 = 0x07FFFFFFu;
+  asm volatile("" : "+v"(k27));
   // This lane's partial of tile k (before the sum over the 16 blocks).
   auto compute_tile = [&](uint32_t k) -> float {
     const uint32_t slice = (t0 + k) / n_rg;
@@ -527,10 +626,11 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     const float f0 = (float)plane_sum(c[0]);
     const float f1 = (float)plane_sum(c[1]);
     // (2s+1) * 2^27 for the sub-block scale s in bits 28-31 of aux_s: the
-    // conversion of s * 2^28 + 2^27 - 1 rounds to (2s+1) * 2^27 exactly
+    // conversion of s * 2^28 + 2^27 - 1 rounds to (2s+1) * 2^27 exactly (one
+    // v_and_or with the low constant in a register: a VOP3 takes one literal)
     const float d = dsc[k];
-    const float ud0 = (float)((words[1] & 0xF0000000u) | 0x07FFFFFFu) * d;
-    const float ud1 = (float)((words[3] & 0xF0000000u) | 0x07FFFFFFu) * d;
+    const float ud0 = (float)((words[1] & 0xF0000000u) | k27) * d;
+    const float ud1 = (float)((words[3] & 0xF0000000u) | k27) * d;
     return fmaf(f1 * ud1, xs[1], (f0 * ud0) * xs[0]);
   };
   // Adds the set-aside terms of activation row mrow (NaN or infinite x) to the
@@ -558,15 +658,31 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     }
   };
   // Row sums of the chunk's tiles for activation row mrow, into out.
+  static_assert(kTilesPerWave == 4, "sum_over_blocks4 reduces four tiles");
   auto reduce_and_store = [&](uint32_t mrow) {
+    if constexpr (!kMulti) {
+      // acc[k] is 0 for k >= cnt
+      const float v = sum_over_blocks4(acc[0], acc[1], acc[2], acc[3]);
+      const uint32_t tk = lane >> 4;  // the tile this lane's row holds
+      uint32_t ofs = 0;
 #pragma unroll
-    for (uint32_t k = 0; k < kTilesPerWave; ++k) {
-      if (k >= cnt) break;  // uniform
-      const uint32_t tau = t0 + k;
-      const uint32_t slice = tau / n_rg;
-      const uint32_t rgl = tau - slice * n_rg;
-      const float v = sum_over_blocks(acc[k]);
-      if (lane < 4) red[(rgl * a.nslices + slice) * 4 + j] = v;
+      for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+        const uint32_t tau = t0 + k;
+        const uint32_t slice = tau / n_rg;  // uniform
+        const uint32_t rgl = tau - slice * n_rg;
+        ofs = tk == k ? (rgl * a.nslices + slice) * 4 : ofs;
+      }
+      if ((lane & 12) == 0 && tk < cnt) red[ofs + j] = v;
+    } else {
+#pragma unroll
+      for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+        if (k >= cnt) break;  // uniform
+        const uint32_t tau = t0 + k;
+        const uint32_t slice = tau / n_rg;
+        const uint32_t rgl = tau - slice * n_rg;
+        const float v = sum_over_blocks(acc[k]);
+        if (lane < 4) red[(rgl * a.nslices + slice) * 4 + j] = v;
+      }
     }
     sync();
     const bool special = *s_special == gen;  // uniform
@@ -589,31 +705,39 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   sync();
   // 2. the first tiles
 #pragma unroll
-  for (uint32_t k = 0; k < kTilesAhead; ++k) q[k] = load_tile(k);
+  for (uint32_t k = 0; k < kTilesEarly; ++k) q[k] = load_tile(k);
   __builtin_amdgcn_sched_barrier(0);
   // 3. tables (waves 0-7), digits (waves from 15 down), scales
   if (tid < 256) {
-    store_grid_row<kWide>(lds, tid, grid_entry_from_code(code));
-    if (!kWide) store_sign_row<kWide>(lds, tid, expand_sign_mask((int)(tid & 127)), 0,
-                                      TL::kSignCopies);
+    store_grid_row<kWide>(lds, tid, code);
+    if (!kWide) store_sign_row<kWide>(lds, tid, sign_mask(tid & 127), 0, TL::kSignCopies);
   } else if (kWide && tid < 512) {
     const uint32_t i = (tid - 256) >> 1, half = tid & 1;
-    store_sign_row<kWide>(lds, i, expand_sign_mask((int)i), half * 16, 16);
+    store_sign_row<kWide>(lds, i, sign_mask(i), half * (TL::kSignCopies / 2),
+                          TL::kSignCopies / 2);
   }
   __builtin_amdgcn_sched_barrier(0);
   digitize_row(0);
   stage_scales();
-  sync();
-  // 4. compute tile k, issue tile k + 2
+  // the rest of the first tiles, then a barrier that leaves them in flight
+  // (the set-up loads were consumed above; the tiles are the last loads issued)
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (uint32_t k = kTilesEarly; k < kTilesAhead; ++k) q[k] = load_tile(k);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kTilesAhead) : "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // 4. once tile k has arrived, issue tile k + kTilesAhead, then compute tile k
   load_tile_scales();
   cur_slice = ~0u;
 #pragma unroll
   for (uint32_t k = 0; k < kTilesPerWave; ++k) {
     acc[k] = 0.0f;
-    if (k < cnt) acc[k] = compute_tile(k);  // uniform
+    asm volatile("" ::"v"(q[k].x), "v"(q[k].y), "v"(q[k].z), "v"(q[k].w));
     __builtin_amdgcn_sched_barrier(0);
     if (k + kTilesAhead < kTilesPerWave) q[k + kTilesAhead] = load_tile(k + kTilesAhead);
     __builtin_amdgcn_sched_barrier(0);
+    if (k < cnt) acc[k] = compute_tile(k);  // uniform
   }
   reduce_and_store(0);
 
@@ -780,6 +904,7 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
   a.bpr = (in_dim + kQK - 1) / kQK;
   a.spr = p.nslices * (kSlicePairs / 4);
   a.spr_magic = (uint32_t)((0x100000000ull + a.spr - 1) / a.spr);
+  a.scale_dw = (a.spr == a.bpr && reinterpret_cast<uintptr_t>(ws) % 4 == 0) ? 1 : 0;
   a.npairs = a.bpr * 4;
   a.nslices = p.nslices;
   a.rg_per_chunk = p.rg_per_chunk;
