@@ -44,6 +44,7 @@ HIP_FLAGS = [
 HIP_SOURCES = [
     "iq2xxs_dequant.hip",
     "iq2xxs_gemv.hip",
+    "iq2xxs_gemv_rows.hip",
     "iq2xxs_gemm.hip",
     "iq2xxs_simple.hip",
     "iq_variants.hip",

@@ -1,4 +1,5 @@
-// iq2xxs_gemv.hip — decode-shaped IQ2_XXS matmul (small m) for gfx950.
+// iq2xxs_gemv.hip — decode-shaped IQ2_XXS matmul, one activation row, for
+// gfx950 (more rows: iq2xxs_gemv_rows.hip).
 //
 // Replaces iq2_xxs_matmul_kernel / iq2_xxs_matmul_w8a8_kernel
 // (src/metal_src/iq2_matmul.metal:188-240, 436-499), which run one thread per
@@ -17,9 +18,9 @@
 //    max|x| < 2^e gives v = rint(x*2^(20-e)) split into three signed 8-bit
 //    digit planes (iq2xxs_device.h), held in LDS.
 //  * Codes expand through two LDS tables: a codebook row holds 16 copies of
-//    {g, -g} (8 magnitude bytes and their negations), a sign row 32 copies of
-//    the 8-byte sign mask; lane l reads copy l & 15 (resp. l & 31), so every
-//    read is free of bank conflicts.  One v_bitop3 (bit select) per dword
+//    {g, -g} (8 magnitude bytes and their negations), a sign row 16 copies of
+//    the 8-byte sign mask; lane l reads copy l & 15, so the 16 lanes the LDS
+//    serves together never share a bank.  One v_bitop3 (bit select) per dword
 //    picks g or -g under the mask.
 //  * v_mfma_i32_4x4x4_16b_i8: in each of the 16 4x4 blocks the A rows are the
 //    three digit planes (the fourth row is unused) and the B columns are 4 weight
@@ -38,28 +39,26 @@
 //   2. every wave issues its first two weight tiles;
 //   3. waves 0-7 build the tables, waves 15, 14, ... digitise, everyone stages
 //      the scales; barrier;
-//   4. each wave computes tile k, then issues tile k+2 (issued after the
-//      compute, the load takes a slot the tile just freed instead of stalling
-//      the wave on a full pipeline before it computes).
+//   4. once tile k has arrived, each wave issues tile k+3 and computes tile k;
+//      a workgroup with more chunks then issues the next chunk's tile k into
+//      the registers tile k has freed, so the next chunk is in flight while
+//      this one is reduced.
 // Weight loads carry the nontemporal hint: every code byte is read once.
 // All waves run the same code with the same sequence of loads, so the
 // compiler's count of outstanding loads (s_waitcnt vmcnt) is exact: a wave
-// waits for exactly the load it is about to use.  The first chunk and row are
-// straight-line code for the same reason; further rows (m > 1) and chunks
-// (large out_dim) loop behind it.
+// waits for exactly the load it is about to use.  The first chunk is
+// straight-line code for the same reason; further chunks (large out_dim) loop
+// behind it.
 //
 // Bound: HBM.  Algorithmic bytes per weight row: ceil(K/256)*66, plus x and
 // out once.
 #include <atomic>
 
 #include "iq2xxs_device.h"
+#include "iq2xxs_gemv_common.h"
 #include "iq2xxs_kernels.h"
 
 namespace cmk {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Lane roles in v_mfma_i32_4x4x4_16b_i8: lane L belongs to 4x4 block L/4; it
 // supplies row L%4 of A and column L%4 of B, and receives column L%4 of C
@@ -74,99 +73,6 @@ constexpr uint32_t kSlicePairs = 16;   // sub-block pairs per tile (one per 4x4 
 constexpr uint32_t kTilesPerWave = 4;  // weight tiles a wave holds
 constexpr uint32_t kTilesEarly = 2;    // tiles issued before the set-up work
 constexpr uint32_t kScaleLoads = 2;    // staged scales per thread and chunk
-constexpr uint32_t kGemvLdsLimit = 160 * 1024;
-// Buffer offset past every num_records used here (buffers are < 2^31 bytes).
-constexpr uint32_t kOutOfRange = 0x80000000u;
-// Word 3 of a gfx9 raw buffer resource (32-bit data format, no swizzle).
-constexpr int kBufferWord3 = 0x00020000;
-// Cache policy of the weight loads: nontemporal (read once).
-constexpr int kStreamLoad = 2;
-
-// Table layouts at LDS offset 0.
-//  wide:   [0, 64K)   codebook row e (256 B) = 16 copies of {g lo, g hi, -g lo, -g hi}
-//          [64K, 80K) sign row i (128 B) = 16 copies of the 8-byte mask of ksigns(i);
-//          the 128-byte stride puts the index of sign field g (bits 7g..7g+6
-//          of aux_s) at address bits 7..13 with one shift and one v_and_or
-//          (field 1 needs no shift)
-//  narrow: [0, 64K)   row r (256 B): bytes [0,128) 8 codebook copies of entry r,
-//          bytes [128, 256) 16 copies of the sign mask of ksigns(r & 127); the
-//          sign index then needs no masking (a byte of aux_s << g carries one
-//          unrelated bit on top), at the price of 2-way bank conflicts.
-// Lane l reads copy l & 15 of a row, so the 16 lanes the LDS serves together
-// hit 16 different bank groups (measured on gfx950 with 16 waves: about 3.0
-// clocks per wave-wide 16-byte read with 16 copies against 4.9 with 8, and
-// 2.6 per 8-byte read with 16 copies against 2.4 with 32).
-template <bool kWide>
-struct GemvTables {
-  static constexpr uint32_t kBytes = kWide ? 80 * 1024 : 64 * 1024;
-  static constexpr uint32_t kGridCopies = kWide ? 16 : 8;
-  static constexpr uint32_t kSignCopies = 16;
-  static constexpr uint32_t kSignBase = kWide ? 65536 : 128;
-  static constexpr uint32_t kSignStride = kWide ? 128 : 256;
-};
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
-                                           kBufferWord3);
-}
-
-// Four level codes (2 bits each, x4 = bits 0..7) as four magnitude bytes
-// {8, 25, 43}: the codes are spread to one per byte with two multiplies
-// (fields 0 and 2, and fields 1 and 3, land in disjoint bits), then select
-// from the byte pool {8, 25, 43, 0} with one v_perm.
-__device__ __forceinline__ uint32_t level_bytes(uint32_t x4) {
-  const uint32_t even = ((x4 & 0x33u) * 0x1001u) & 0x00030003u;   // codes 0, 2 -> bytes 0, 2
-  const uint32_t odd = ((x4 & 0xCCu) * 0x40040u) & 0x03000300u;   // codes 1, 3 -> bytes 1, 3
-  return __builtin_amdgcn_perm(0u, 0x002B1908u, even | odd);
-}
-
-// Bit j of the nibble n as byte j of the result: 0xFF where set.  The nibble's
-// copies at shifts 0, 7, 14, 21 do not overlap, so the multiply places bit j at
-// bit 8j without carries.
-__device__ __forceinline__ uint32_t byte_mask4(uint32_t n) {
-  const uint32_t t = (n * 0x00204081u) & 0x01010101u;
-  return (t << 8) - t;
-}
-
-// All copies of codebook row e (code c: 2-bit level codes of its 8 bytes); the
-// copy order is rotated by e so the 16 lanes the LDS serves together write 16
-// different bank groups.
-template <bool kWide>
-__device__ __forceinline__ void store_grid_row(uint8_t* lds, uint32_t e, uint32_t c) {
-  const uint32_t lo = level_bytes(c & 0xFFu), hi = level_bytes(c >> 8);
-  // per-byte negation: (~g) + 1 never carries across bytes since g >= 8
-  const u32x4 v = {lo, hi, ~lo + 0x01010101u, ~hi + 0x01010101u};
-  constexpr uint32_t C = GemvTables<kWide>::kGridCopies;
-  const uint32_t row = e * 256, rot = 16 * e;
-#pragma unroll
-  for (uint32_t k = 0; k < C; ++k)
-    *reinterpret_cast<u32x4*>(lds + (row | ((rot + 16 * k) & (16 * C - 16)))) = v;
-}
-
-// The 8-byte mask of ksigns(i) = i | parity(i) << 7.
-__device__ __forceinline__ u32x2 sign_mask(uint32_t i) {
-  const uint32_t sb = i | ((__popc(i) & 1u) << 7);
-  return u32x2{byte_mask4(sb & 0xFu), byte_mask4(sb >> 4)};
-}
-
-// Copies [k0, k0 + n) of sign row i (rotated like the codebook rows).
-template <bool kWide>
-__device__ __forceinline__ void store_sign_row(uint8_t* lds, uint32_t i, u32x2 v, uint32_t k0,
-                                               uint32_t n) {
-  using TL = GemvTables<kWide>;
-  constexpr uint32_t C = TL::kSignCopies;
-  uint8_t* const row = lds + TL::kSignBase + i * TL::kSignStride;
-#pragma unroll
-  for (uint32_t k = k0; k < k0 + n; ++k)
-    *reinterpret_cast<u32x2*>(row + 8 * ((k + i) & (C - 1))) = v;
-}
-
-// Table address  256 * byte G of w + low byte of cbase  as one v_perm
-// (result bytes: cbase.b0, w.bG, 0, 0).
-template <int G>
-__device__ __forceinline__ uint32_t perm_addr(uint32_t w, uint32_t cbase) {
-  return __builtin_amdgcn_perm(w, cbase, 0x0C0C0000u | ((0x04u + G) << 8));
-}
 
 // Sign-row address of group G of aux_s for this lane's copy base cs (whose
 // bits 7..13 are clear).
@@ -180,35 +86,11 @@ __device__ __forceinline__ uint32_t sign_addr(uint32_t aux_s, uint32_t cs) {
   }
 }
 
-// LDS reads at byte addresses (the kernel's dynamic LDS starts at 0).
-__device__ __forceinline__ u32x2 lds_u2(uint32_t addr) {
-  return *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
-      static_cast<uintptr_t>(addr));
-}
-__device__ __forceinline__ u32x4 lds_u4(uint32_t addr) {
-  return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
-      static_cast<uintptr_t>(addr));
-}
-
-// Bits of a where m is set, of b elsewhere (one v_bitop3 on gfx950).  Kept in
-// plain C: the result feeds v_mfma, and only compiler-visible instructions
-// get the VALU-write -> MFMA-read wait states inserted.
-__device__ __forceinline__ uint32_t bit_select(uint32_t m, uint32_t a, uint32_t b) {
-  return (m & a) | (~m & b);
-}
-
 // 65536 c[2] + 256 c[1] + c[0] in 32-bit arithmetic (exact when the result
 // fits in an int32).
 __device__ __forceinline__ int plane_sum(v4i c) {
   const uint32_t hi = ((uint32_t)c[2] << 8) + (uint32_t)c[1];
   return (int)((hi << 8) + (uint32_t)c[0]);
-}
-
-// Makes v look modified here (emits no instruction): the decode of a tile's
-// codes cannot be hoisted out of the activation-row loop (m > 1), where it
-// would hold every decoded tile in registers at once.
-__device__ __forceinline__ void pin_here(u32x4& v) {
-  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
 }
 
 // Sum over the 16 lanes that share lane & 3 (the 16 4x4 blocks) of one
@@ -250,54 +132,6 @@ __device__ __forceinline__ float sum_over_blocks4(float a0, float a1, float a2, 
   return v;
 }
 
-// Max over the 4 lanes of an aligned quad (DPP quad_perm [1,0,3,2], [2,3,0,1]).
-__device__ __forceinline__ uint32_t quad_max_u32(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
-  return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
-}
-
-// Eight consecutive activations (one digitisation task) by buffer loads.  An
-// absent task or element reads at an offset past the buffer and gets zeros,
-// with no branch, so the count of outstanding loads is the same on every path.
-// kVec: the 8 elements are 16-byte aligned and in_dim % 8 == 0.
-template <int XD, bool kVec>
-struct XTask {
-  static constexpr uint32_t kRegs = (kVec && XD != 0) ? 4 : 8;
-  uint32_t raw[kRegs];
-
-  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t rx, uint32_t elem0, uint32_t c0,
-                                       uint32_t in_dim, bool valid) {
-    constexpr uint32_t es = XD == 0 ? 4 : 2;
-    if constexpr (kVec) {
-      const uint32_t off = valid ? elem0 * es : kOutOfRange;
-      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
-      raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
-      if constexpr (XD == 0) {
-        const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(rx, off + 16, 0, 0);
-        raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
-      }
-    } else {
-#pragma unroll
-      for (uint32_t k = 0; k < 8; ++k) {
-        const uint32_t off = (valid && c0 + k < in_dim) ? (elem0 + k) * es : kOutOfRange;
-        if constexpr (XD == 0)
-          raw[k] = __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0);
-        else
-          raw[k] = __builtin_amdgcn_raw_buffer_load_b16(rx, off, 0, 0);
-      }
-    }
-  }
-
-  __device__ __forceinline__ float get(int k) const {
-    uint32_t b;
-    if constexpr (kVec && XD != 0)
-      b = (k & 1) ? (raw[k >> 1] >> 16) : (raw[k >> 1] & 0xFFFFu);
-    else
-      b = raw[k];
-    return x_bits_to_float<XD>(b);
-  }
-};
-
 struct GemvArgs {
   const void* x;
   const uint8_t* wb;
@@ -321,17 +155,15 @@ struct GemvArgs {
 
 // XD: activation dtype (0 f32, 1 f16, 2 bf16); kVecX: activations can be read
 // as aligned 16-byte vectors; kWide: table layout; kXT: digitisation tasks
-// per thread per round; kW8A8: fake-quantise x per row first; kMulti: m > 1,
-// more than one chunk per workgroup or more than one digitisation round (the
-// loops are compiled out otherwise).
+// per thread per round; kW8A8: fake-quantise x per row first; kMulti: more
+// than one chunk per workgroup or more than one digitisation round (the loops
+// are compiled out otherwise).
 template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti>
 __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   using TL = GemvTables<kWide>;
-  // Tiles in flight ahead of the one computed: three for one chunk and row;
-  // the looping kernels keep two (a third would exceed the 128 VGPRs a wave of
-  // a 1024-thread workgroup has and spill).
-  constexpr uint32_t kTilesAhead = kMulti ? 2 : 3;
+  // Tiles in flight ahead of the one computed.
+  constexpr uint32_t kTilesAhead = 3;
   uint16_t* sscale = reinterpret_cast<uint16_t*>(lds + a.scale_ofs);
   float* xsc = reinterpret_cast<float*>(lds + a.xsc_ofs);
   uint8_t* xdig = lds + a.xdig_ofs;
@@ -355,19 +187,31 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.ws, a.ws_records);
   const uint32_t round = kGemvThreads * kXT;  // tasks per digitisation round
 
-  // ---- chunk geometry and this wave's tiles
-  uint32_t chunk = blockIdx.x;
-  uint32_t row_begin, n_rg, rows, t0, cnt;
-  auto set_chunk = [&](uint32_t c) {
+  // ---- chunk geometry and this wave's tiles (all uniform)
+  struct ChunkGeom {
+    uint32_t row_begin, n_rg, rows, t0, cnt;
+  };
+  auto geom_of = [&](uint32_t c) {
+    ChunkGeom g;
     const uint32_t rg_begin = c * a.rg_per_chunk;
     const uint32_t rg_end = min(rg_begin + a.rg_per_chunk, n_rg_total);
-    n_rg = rg_end - rg_begin;
-    row_begin = rg_begin * 4;
-    rows = min(rg_end * 4, a.out_dim) - row_begin;
-    const uint32_t ntiles = n_rg * a.nslices;
+    g.n_rg = rg_end - rg_begin;
+    g.row_begin = rg_begin * 4;
+    g.rows = min(rg_end * 4, a.out_dim) - g.row_begin;
+    const uint32_t ntiles = g.n_rg * a.nslices;
     const uint32_t base = ntiles / kGemvWaves, extra = ntiles - base * kGemvWaves;
-    cnt = base + (wave < extra ? 1u : 0u);
-    t0 = wave * base + min(wave, extra);
+    g.cnt = base + (wave < extra ? 1u : 0u);
+    g.t0 = wave * base + min(wave, extra);
+    return g;
+  };
+  uint32_t chunk = blockIdx.x;
+  uint32_t row_begin, n_rg, rows, t0, cnt;  // the current chunk's
+  auto set_chunk = [&](const ChunkGeom& g) {
+    row_begin = g.row_begin;
+    n_rg = g.n_rg;
+    rows = g.rows;
+    t0 = g.t0;
+    cnt = g.cnt;
   };
   // Lane (b, j) loads pair b of row j of the tile: byte offset
   // (first row of the tile's row group) * row_bytes + slice * 256 (uniform)
@@ -376,20 +220,25 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // codes, whose staged scale d is 0; tiles past this wave's count are sent
   // past the buffer.
   const uint32_t tile_lane_ofs = j * row_bytes + 16 * b;
-  auto load_tile = [&](uint32_t k) -> u32x4 {
-    const uint32_t tau = t0 + k;
-    const uint32_t slice = tau / n_rg;
-    const uint32_t rgl = tau - slice * n_rg;
-    const uint32_t base = k < cnt ? (row_begin + rgl * 4) * row_bytes + slice * (kSlicePairs * 16)
-                                  : kOutOfRange;  // uniform
+  auto load_tile_of = [&](const ChunkGeom& g, uint32_t k) -> u32x4 {
+    const uint32_t tau = g.t0 + k;
+    const uint32_t slice = tau / g.n_rg;
+    const uint32_t rgl = tau - slice * g.n_rg;
+    const uint32_t base = k < g.cnt
+                              ? (g.row_begin + rgl * 4) * row_bytes + slice * (kSlicePairs * 16)
+                              : kOutOfRange;  // uniform
     return __builtin_amdgcn_raw_buffer_load_b128(rw, base + tile_lane_ofs, 0, kStreamLoad);
+  };
+  auto load_tile = [&](uint32_t k) -> u32x4 {
+    return load_tile_of(ChunkGeom{row_begin, n_rg, rows, t0, cnt}, k);
   };
   // Super-block scales of the chunk, staged as rows of a.spr entries (blocks
   // padded to whole slices) with zeros for padding rows and blocks.
   uint32_t sraw[kScaleLoads];
   // (the looping kernels keep the 2-byte loads and the one-tile reductions:
   // they are at the 128-VGPR limit, and the alternatives cost spills)
-  auto load_scales = [&]() {
+  auto load_scales_of = [&](const ChunkGeom& g) {
+    const uint32_t row_begin = g.row_begin, rows = g.rows;
     if (!kMulti && a.scale_dw) {
       // a chunk's scales are contiguous and staged as they lie: rows*bpr/2
       // dwords (rows is a multiple of 4 or the chunk ends the matrix, and bpr is
@@ -412,6 +261,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
           rs, ok ? ((row_begin + rl) * a.bpr + blk) * kScalesPerBlock : kOutOfRange, 0, 0);
     }
   };
+  auto load_scales = [&]() { load_scales_of(ChunkGeom{row_begin, n_rg, rows, t0, cnt}); };
   auto stage_scales = [&]() {
     const uint32_t nstaged = a.rg_per_chunk * 4 * a.spr;
     if (!kMulti && a.scale_dw) {
@@ -588,7 +438,6 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         xr[h][4] = hi.x; xr[h][5] = hi.y; xr[h][6] = hi.z; xr[h][7] = hi.w;
       }
     }
-    if constexpr (kMulti) pin_here(q[k]);
     const uint32_t words[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
     // signed int8 weights of both sub-blocks: g where the mask is clear, -g where set
     uint32_t w[2][8];
@@ -695,8 +544,11 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     if (special) fix_up_special(mrow);
   };
 
-  // ======== first chunk, activation row 0 (straight-line) ========
-  set_chunk(chunk);
+  // ======== first chunk (straight-line) ========
+  set_chunk(geom_of(chunk));
+  // the next chunk of this workgroup (looping kernels only)
+  uint32_t next = chunk + gridDim.x;
+  ChunkGeom gn = geom_of(kMulti && next < a.nchunks ? next : chunk);
   // 1. set-up loads, ahead of every weight load
   const uint32_t code = tid < 256 ? kGridCodesDev[tid] : 0u;
   if (tid == 0) *s_special = 0;
@@ -738,44 +590,36 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     if (k + kTilesAhead < kTilesPerWave) q[k + kTilesAhead] = load_tile(k + kTilesAhead);
     __builtin_amdgcn_sched_barrier(0);
     if (k < cnt) acc[k] = compute_tile(k);  // uniform
+    if constexpr (kMulti) {
+      // tile k's registers are free: the next chunk's scales (once), then its tile k
+      if (next < a.nchunks) {
+        if (k == 0) load_scales_of(gn);
+        q[k] = load_tile_of(gn, k);
+      }
+    }
   }
   reduce_and_store(0);
 
-  // ======== further activation rows and chunks ========
+  // ======== further chunks (large out_dim): their tiles are in flight ========
   if constexpr (!kMulti) return;
-  for (;;) {
-    for (uint32_t mrow = 1; mrow < a.m; ++mrow) {
-      sync();  // digits and partial sums are rewritten
-      load_x(0, mrow);
-      digitize_row(mrow);
-      sync();
-      cur_slice = ~0u;
-#pragma unroll
-      for (uint32_t k = 0; k < kTilesPerWave; ++k) {
-        acc[k] = 0.0f;
-        if (k < cnt) acc[k] = compute_tile(k);
-      }
-      reduce_and_store(mrow);
-    }
-    chunk += gridDim.x;
-    if (chunk >= a.nchunks) break;
-    set_chunk(chunk);
-    load_scales();
-#pragma unroll
-    for (uint32_t k = 0; k < kTilesPerWave; ++k) q[k] = load_tile(k);
-    sync();  // scales and partial sums of the previous chunk consumed
+  while (next < a.nchunks) {
+    chunk = next;
+    set_chunk(gn);
+    next = chunk + gridDim.x;
+    if (next < a.nchunks) gn = geom_of(next);
+    sync();  // the previous chunk's scales and partial sums are consumed
     stage_scales();
-    if (a.m > 1) {
-      load_x(0, 0);
-      digitize_row(0);
-    }
     sync();
     load_tile_scales();
     cur_slice = ~0u;
 #pragma unroll
     for (uint32_t k = 0; k < kTilesPerWave; ++k) {
       acc[k] = 0.0f;
-      if (k < cnt) acc[k] = compute_tile(k);
+      if (k < cnt) acc[k] = compute_tile(k);  // uniform
+      if (next < a.nchunks) {
+        if (k == 0) load_scales_of(gn);
+        q[k] = load_tile_of(gn, k);
+      }
     }
     reduce_and_store(0);
   }
@@ -842,6 +686,7 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
 }
 
 bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
+  if (m > 1) return gemv_rows_supported(m < 8 ? m : 8, out_dim, in_dim, x_dtype);
   GemvPlan p;
   return plan_gemv(m, out_dim, in_dim, x_dtype, 1, &p);
 }
@@ -865,7 +710,7 @@ static hipError_t launch_gemv_t(const GemvArgs& a, const GemvPlan& p, hipStream_
 
 template <int XD, bool V, bool W, bool Q>
 static hipError_t launch_gemv_m(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
-  const bool multi = a.m > 1 || a.nchunks > p.grid || a.ntasks > kGemvThreads * p.xt;
+  const bool multi = a.nchunks > p.grid || a.ntasks > kGemvThreads * p.xt;
   if (multi)
     return p.xt <= 1 ? launch_gemv_t<XD, V, W, 1, Q, true>(a, p, stream)
                      : launch_gemv_t<XD, V, W, 2, Q, true>(a, p, stream);
@@ -891,6 +736,18 @@ static hipError_t launch_gemv_v(const GemvArgs& a, const GemvPlan& p, bool vec,
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream) {
+  if (m > 1) {
+    // groups of up to 8 activation rows, each decoding the weights once
+    const size_t esize = x_dtype == 0 ? 4 : 2;
+    for (uint32_t r0 = 0; r0 < m; r0 += 8) {
+      const hipError_t e = launch_iq2xxs_gemv_rows(
+          static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize, x_dtype,
+          m - r0 < 8 ? m - r0 : 8, wb, ws, out + (size_t)r0 * out_dim, out_dim, in_dim, w8a8,
+          num_cus, stream);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   GemvPlan p;
   if (!plan_gemv(m, out_dim, in_dim, x_dtype, num_cus, &p)) return hipErrorInvalidValue;
   GemvArgs a;

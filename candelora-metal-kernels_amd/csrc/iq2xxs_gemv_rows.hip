@@ -1,0 +1,504 @@
+// iq2xxs_gemv_rows.hip — IQ2_XXS matmul for 2..8 activation rows on gfx950.
+//
+// Replaces iq2_xxs_matmul_kernel / iq2_xxs_matmul_w8a8_kernel
+// (src/metal_src/iq2_matmul.metal:188-240, 436-499) for small m > 1.  The
+// reference runs one thread per output, so every weight is decoded once per
+// activation row; here a weight is decoded once per launch and one MFMA
+// multiplies it against all the rows.
+//
+// Arithmetic.  The activations become the same exact integer digits as in the
+// one-row kernel (iq2xxs_gemv.hip): per 32-column sub-block, three signed 8-bit
+// planes of rint(x * 2^(20-e)), in LDS.  The codes expand through the same
+// LDS tables ({g, -g} codebook rows, 8-byte sign masks, one bit select per
+// dword).  v_mfma_i32_32x32x32_i8 then takes
+//   A: 32 rows = 8 activation rows x 4 digit planes (plane 3 and absent rows
+//      read a zero plane), 32 columns = one sub-block;
+//   B: the same 32 columns of 32 weight rows.
+// Lane l supplies A row l%32 and B column (weight row) l%32, both over columns
+// 16*(l/32) .. +15 of the sub-block (so A and B agree on the k order whatever
+// the hardware's byte order is), and receives C rows 8*(r/4) + 4*(l/32) + r%4
+// in register r: planes 0..2 of activation rows 2t + l/32 (t = r/4) against
+// weight row l%32.  The three plane sums combine exactly in int32; the scale
+// (2s+1) * 2^(e-23) is applied in fp32 per sub-block, d once per super-block.
+//
+// Work split.  A *unit* is 32 weight rows x half a super-block (4 sub-blocks,
+// 1 KB of codes: one 16-byte load per lane).  A workgroup of 16 waves owns a
+// chunk of R consecutive 32-row groups; the P = 16/R waves of a row group share
+// its units.  K is processed in slices of S super-blocks whose digits fit in
+// LDS next to the tables; a wave holds at most kU units per slice and
+// prefetches the next slice's unit into the registers of the one it has just
+// unpacked.  The waves of a row group add their partial sums in wave order,
+// so results are deterministic.
+//
+// Bound: HBM (the same algorithmic bytes as the one-row kernel; every weight
+// byte is read once, x once per workgroup from L2).
+#include <atomic>
+
+#include "iq2xxs_device.h"
+#include "iq2xxs_gemv_common.h"
+#include "iq2xxs_kernels.h"
+
+namespace cmk {
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t kRowsWaves = 16;
+constexpr uint32_t kRowsThreads = kRowsWaves * 64;
+constexpr uint32_t kRowsMaxTasks = 2;  // digitisation tasks per thread and slice
+constexpr uint32_t kRowsFlagBytes = 1024;
+using RowsTables = GemvTables<true>;
+
+struct RowsArgs {
+  const void* x;
+  const uint8_t* wb;
+  const uint8_t* ws;
+  float* out;
+  uint32_t m, out_dim, in_dim, bpr;
+  uint32_t n_rg;         // 32-row groups
+  uint32_t rg_shift;     // log2 of the row groups per chunk (R)
+  uint32_t nchunks;
+  uint32_t slice_shift;  // log2 of the super-blocks per K slice (S)
+  uint32_t nslices;
+  uint32_t wb_records, ws_records, x_records;  // bytes addressable by the buffer loads
+  uint32_t plane_stride;                       // LDS bytes between digit planes
+  uint32_t xdig_ofs, xsc_ofs, flag_ofs;        // LDS layout; partial sums reuse xdig
+};
+
+// Units a wave holds per slice: four for up to 4 rows read as vectors, two
+// otherwise (the registers a 1024-thread workgroup leaves a wave: 128).
+constexpr uint32_t rows_units(int rows, bool vec) { return rows == 4 && vec ? 4 : 2; }
+
+// XD: activation dtype (0 f32, 1 f16, 2 bf16); kVecX: activations can be read
+// as aligned 16-byte vectors; kW8A8: fake-quantise x per row first; kRows: 4
+// or 8, at least m.
+template <int XD, bool kVecX, bool kW8A8, int kRows>
+__global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr uint32_t kT = kRows / 2;  // activation rows per lane: 2t + h
+  constexpr uint32_t kU = rows_units(kRows, kVecX);
+  uint8_t* xdig = lds + a.xdig_ofs;
+  float* xsc = reinterpret_cast<float*>(lds + a.xsc_ofs);
+  float* red = reinterpret_cast<float*>(lds + a.xdig_ofs);
+  uint32_t* s_kinds = reinterpret_cast<uint32_t*>(lds + a.xdig_ofs);
+  uint32_t* s_special = reinterpret_cast<uint32_t*>(lds + a.flag_ofs);  // bit r: row r not finite
+  float* s_inv = reinterpret_cast<float*>(lds + a.flag_ofs + 16);      // W8A8 scales, 8 rows
+  float* s_wred = reinterpret_cast<float*>(lds + a.flag_ofs + 64);     // 16 waves x 8 rows
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t h = lane >> 5;  // column half of the sub-block / activation row parity
+  const uint32_t n = lane & 31;  // weight row in the group
+  const uint32_t R = 1u << a.rg_shift;
+  const uint32_t P = kRowsWaves >> a.rg_shift;  // waves per row group
+  const uint32_t rgl = wave >> (4 - a.rg_shift);
+  const uint32_t wp = wave & (P - 1);
+  const uint32_t S = 1u << a.slice_shift;
+  const uint32_t row_bytes = a.bpr * kBytesPerBlock;
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, a.x_records);
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.wb, a.wb_records);
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.ws, a.ws_records);
+  auto sync = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- W8A8 row scales (iq2_matmul.metal:86-96): 127 / max|x_r|
+  if constexpr (kW8A8) {
+    float mx[kRows];
+#pragma unroll
+    for (uint32_t r = 0; r < (uint32_t)kRows; ++r) mx[r] = 0.0f;
+    for (uint32_t c = tid; c < a.in_dim; c += kRowsThreads)
+#pragma unroll
+      for (uint32_t r = 0; r < (uint32_t)kRows; ++r)
+        if (r < a.m)
+          mx[r] = fmaxf(mx[r], fabsf(x_bits_to_float<XD>(
+                                   load_x_bits<XD>(a.x, (size_t)r * a.in_dim + c))));
+#pragma unroll
+    for (uint32_t r = 0; r < (uint32_t)kRows; ++r) {
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off));
+      if (lane == 0) s_wred[wave * 8 + r] = mx[r];
+    }
+    sync();
+    if (tid < (uint32_t)kRows) {
+      float v = 0.0f;
+      for (uint32_t w = 0; w < kRowsWaves; ++w) v = fmaxf(v, s_wred[w * 8 + tid]);
+      s_inv[tid] = (v < 1e-8f) ? 1.0f : 127.0f / v;
+    }
+    sync();
+  }
+
+  // ---- per-lane constants
+  const uint32_t cg = 16 * (lane & 15);                          // codebook copy
+  const uint32_t cs = RowsTables::kSignBase + 8 * (lane & 15);   // sign-mask copy
+  const uint32_t sel0 = 0x0C0C0000u | ((4u + 2u * h) << 8);      // codebook byte 2h of aux_g
+  const uint32_t sel1 = sel0 + 0x100u;                           // byte 2h + 1
+  const uint32_t rot0 = h ? 7u : 25u, rot1 = h ? 14u : 0u;       // sign fields 2h, 2h + 1
+  uint32_t k27 = 0x07FFFFFFu;
+  asm volatile("" : "+v"(k27));
+  // A row l%32 = (activation row, plane); plane 3 and absent rows read zeros
+  const uint32_t ai = lane & 31, axr = ai >> 2, ap = ai & 3;
+  const uint32_t aplane = (ap == 3 || axr >= a.m) ? 3u * kRows : axr * 3 + ap;
+  const uint32_t a_base = a.xdig_ofs + aplane * a.plane_stride + 16 * h;
+  const uint32_t xs_base = a.xsc_ofs + h * kT * 4;
+
+  // ---- digitisation of one K slice: task = row * (32 S) + 8-column group
+  XTask<XD, kVecX> xo[kRowsMaxTasks];
+  auto load_x = [&](uint32_t s) {
+    const uint32_t sb0 = s << a.slice_shift;
+    const uint32_t s_eff = min(S, a.bpr - sb0);
+#pragma unroll
+    for (uint32_t u = 0; u < kRowsMaxTasks; ++u) {
+      const uint32_t task = u * kRowsThreads + tid;
+      const uint32_t xrow = task >> (a.slice_shift + 5);
+      const uint32_t col8 = task & (32 * S - 1);
+      const uint32_t c0 = sb0 * kQK + col8 * 8;
+      const bool ok = s < a.nslices && xrow < a.m && col8 < 32 * s_eff && c0 < a.in_dim;
+      xo[u].load(rx, xrow * a.in_dim + c0, c0, a.in_dim, ok);
+    }
+  };
+  auto digitize = [&](uint32_t s) {
+    const uint32_t sb0 = s << a.slice_shift;
+    const uint32_t s_eff = min(S, a.bpr - sb0);
+#pragma unroll
+    for (uint32_t u = 0; u < kRowsMaxTasks; ++u) {
+      const uint32_t task = u * kRowsThreads + tid;
+      const uint32_t xrow = task >> (a.slice_shift + 5);
+      const uint32_t col8 = task & (32 * S - 1);
+      const bool ok = xrow < a.m && col8 < 32 * s_eff;  // same on the 4 lanes of a quad
+      float inv = 1.0f;
+      if constexpr (kW8A8) inv = s_inv[min(xrow, 7u)];
+      float xv[8];
+      uint32_t mb = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        xv[k] = xo[u].get(k);
+        if constexpr (kW8A8) xv[k] = qdq_w8a8(xv[k], inv);
+        mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
+      }
+      mb = quad_max_u32(mb);
+      if (mb >= kInfBits) {  // a NaN or an infinity: set aside (fixed up at the end)
+        mb = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t ab = __float_as_uint(xv[k]) & kAbsMask;
+          if (ab >= kInfBits) xv[k] = 0.0f;
+          mb = max(mb, ab < kInfBits ? ab : 0u);
+        }
+        mb = quad_max_u32(mb);
+        if (ok) atomicOr(s_special, 1u << xrow);
+      }
+      if (ok) {
+        const int e = digit_exponent(__uint_as_float(mb));
+        const float scale = ldexpf(1.0f, kDigitShift - e);
+        uint32_t dg[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dg[k] = digitize_biased(xv[k], scale);
+        uint32_t p0[2], p1[2], p2[2];
+        digits_to_planes(dg[0], dg[1], dg[2], dg[3], p0[0], p1[0], p2[0]);
+        digits_to_planes(dg[4], dg[5], dg[6], dg[7], p0[1], p1[1], p2[1]);
+        uint8_t* dst = xdig + xrow * 3 * a.plane_stride + col8 * 8;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(p0[0] ^ 0x80808080u, p0[1] ^ 0x80808080u);
+        *reinterpret_cast<uint2*>(dst + a.plane_stride) =
+            make_uint2(p1[0] ^ 0x80808080u, p1[1] ^ 0x80808080u);
+        *reinterpret_cast<uint2*>(dst + 2 * a.plane_stride) =
+            make_uint2(p2[0] ^ 0x80808080u, p2[1] ^ 0x80808080u);
+        if ((col8 & 3) == 0)
+          xsc[(col8 >> 2) * kRows + (xrow & 1) * kT + (xrow >> 1)] =
+              ldexpf(1.0f, e - kDigitShift - 3);
+      }
+    }
+  };
+
+  // ---- weight units: this wave's t-th unit of slice s is half-super-block
+  // ul = wp + P * t of the slice (super-block s * S + ul / 2, half ul % 2);
+  // lane (n, h) loads pair 2 (ul % 2) + h of row n
+  u32x4 q[kU];
+  uint32_t draw[kU];
+  uint32_t row0 = 0;
+  auto issue_unit = [&](uint32_t s, uint32_t t) {
+    const uint32_t sb0 = s << a.slice_shift;
+    const uint32_t ul = wp + P * t;
+    const uint32_t row = row0 + n;
+    const bool ok = s < a.nslices && ul < 2 * min(S, a.bpr - sb0) && row < a.out_dim;
+    const uint32_t sb = sb0 + (ul >> 1);
+    const uint32_t off =
+        ok ? row * row_bytes + sb * kBytesPerBlock + (ul & 1) * 32 + 16 * h : kOutOfRange;
+    q[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kStreamLoad);
+    draw[t] = __builtin_amdgcn_raw_buffer_load_b16(
+        rs, ok ? (row * a.bpr + sb) * kScalesPerBlock : kOutOfRange, 0, 0);
+  };
+
+  float acc[kT];
+  bool tables_ready = false;
+  for (uint32_t chunk = blockIdx.x; chunk < a.nchunks; chunk += gridDim.x) {
+    if (chunk != blockIdx.x) sync();  // the previous chunk's flags are read
+    row0 = (chunk * R + rgl) * 32;
+    const uint32_t code = (!tables_ready && tid < 256) ? kGridCodesDev[tid] : 0u;
+    if (tid == 0) *s_special = 0;
+    // set-up loads ahead of the weights: the first slice's activations
+    load_x(0);
+#pragma unroll
+    for (uint32_t t = 0; t < kU; ++t) issue_unit(0, t);
+    if (!tables_ready) {
+      if (tid < 256) {
+        store_grid_row<true>(lds, tid, code);
+      } else if (tid < 512) {
+        const uint32_t i = (tid - 256) >> 1, half = tid & 1;
+        store_sign_row<true>(lds, i, sign_mask(i), half * (RowsTables::kSignCopies / 2),
+                             RowsTables::kSignCopies / 2);
+      }
+      tables_ready = true;
+    }
+#pragma unroll
+    for (uint32_t t = 0; t < kT; ++t) acc[t] = 0.0f;
+
+    for (uint32_t s = 0; s < a.nslices; ++s) {
+      if (s > 0) load_x(s);  // (the first slice's activations were loaded above)
+      sync();  // the previous slice's digits are consumed (first slice: the flag is clear)
+      // the zero plane (its area is rewritten by the partial sums at the end)
+      if (tid < 16 * S)
+        *reinterpret_cast<u32x4*>(xdig + 3 * kRows * a.plane_stride + 16 * tid) =
+            u32x4{0, 0, 0, 0};
+      digitize(s);
+      sync();
+      const uint32_t sb0 = s << a.slice_shift;
+      const uint32_t s_eff = min(S, a.bpr - sb0);
+#pragma unroll
+      for (uint32_t t = 0; t < kU; ++t) {
+        const uint32_t ul = wp + P * t;
+        if (ul >= 2 * s_eff) break;  // uniform
+        // words of the unit's 4 sub-blocks for this lane's row: lane (n, 0)
+        // holds the unit's first pair, lane (n, 1) its second; v_permlane32_swap
+        // of a register with itself gives every lane both halves' values
+        uint32_t gw[4], sw[4];
+#pragma unroll
+        for (uint32_t c = 0; c < 4; ++c) {
+          const auto r = __builtin_amdgcn_permlane32_swap(q[t][c], q[t][c], false, false);
+          const uint32_t j0 = c >> 1, j1 = j0 + 2;
+          if (c & 1) {
+            sw[j0] = r[0];
+            sw[j1] = r[1];
+          } else {
+            gw[j0] = r[0];
+            gw[j1] = r[1];
+          }
+        }
+        const float dq = half_bits_to_float((uint16_t)draw[t]) * 0x1p-27f;
+        issue_unit(s + 1, t);  // the registers are free: prefetch
+        float au[kT];
+#pragma unroll
+        for (uint32_t tt = 0; tt < kT; ++tt) au[tt] = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          const uint32_t sub = ul * 4 + j;  // sub-block in the slice
+          const uint32_t ga0 = __builtin_amdgcn_perm(gw[j], cg, sel0);
+          const uint32_t ga1 = __builtin_amdgcn_perm(gw[j], cg, sel1);
+          const uint32_t sa0 = (__builtin_amdgcn_alignbit(sw[j], sw[j], rot0) & 0x3F80u) | cs;
+          const uint32_t sa1 = (__builtin_amdgcn_alignbit(sw[j], sw[j], rot1) & 0x3F80u) | cs;
+          const u32x4 g0 = lds_u4(ga0), g1 = lds_u4(ga1);
+          const u32x2 m0 = lds_u2(sa0), m1 = lds_u2(sa1);
+          const u32x4 av = lds_u4(a_base + sub * 32);
+          const v4i bw = {(int)bit_select(m0.x, g0.z, g0.x), (int)bit_select(m0.y, g0.w, g0.y),
+                          (int)bit_select(m1.x, g1.z, g1.x), (int)bit_select(m1.y, g1.w, g1.y)};
+          const v4i aw = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+          const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bw, v16i{}, 0, 0, 0);
+          // (2s+1) * 2^27 (see the one-row kernel), times the activation scales
+          const float sj = (float)((sw[j] & 0xF0000000u) | k27);
+          float xs[kT];
+          if constexpr (kT == 4) {
+            const u32x4 v = lds_u4(xs_base + sub * kRows * 4);
+            xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
+            xs[2] = __uint_as_float(v.z); xs[3] = __uint_as_float(v.w);
+          } else {
+            const u32x2 v = lds_u2(xs_base + sub * kRows * 4);
+            xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
+          }
+#pragma unroll
+          for (uint32_t tt = 0; tt < kT; ++tt) {
+            const uint32_t hi = ((uint32_t)c[4 * tt + 2] << 8) + (uint32_t)c[4 * tt + 1];
+            const float f = (float)(int)((hi << 8) + (uint32_t)c[4 * tt]);
+            au[tt] = fmaf(f, sj * xs[tt], au[tt]);
+          }
+        }
+#pragma unroll
+        for (uint32_t tt = 0; tt < kT; ++tt) acc[tt] = fmaf(au[tt], dq, acc[tt]);
+      }
+    }
+
+    // ---- the P waves of a row group add their partial sums in wave order
+    sync();
+#pragma unroll
+    for (uint32_t tt = 0; tt < kT; ++tt) red[((rgl * P + wp) * kT + tt) * 64 + lane] = acc[tt];
+    sync();
+    const uint32_t chunk_row0 = chunk * R * 32;
+    for (uint32_t o = tid; o < R * kT * 64; o += kRowsThreads) {
+      const uint32_t ol = o & 63, tt = (o >> 6) % kT, rg = (o >> 6) / kT;
+      float sum = 0.0f;
+      for (uint32_t w = 0; w < P; ++w) sum += red[((rg * P + w) * kT + tt) * 64 + ol];
+      const uint32_t xrow = 2 * tt + (ol >> 5), row = chunk_row0 + rg * 32 + (ol & 31);
+      if (xrow < a.m && row < a.out_dim) a.out[(size_t)xrow * a.out_dim + row] = sum;
+    }
+
+    // ---- rows that held a NaN or an infinity: add the kind of the
+    // set-aside terms x_c * w_rc to the chunk's outputs
+    sync();
+    const uint32_t special = *s_special;  // uniform
+    if (special) {
+      const uint32_t rows = min(R * 32, a.out_dim - min(chunk_row0, a.out_dim));
+      for (uint32_t xrow = 0; xrow < a.m; ++xrow) {
+        if (!((special >> xrow) & 1u)) continue;
+        for (uint32_t rl = tid; rl < rows; rl += kRowsThreads) s_kinds[rl] = 0;
+        sync();
+        float inv = 1.0f;
+        if constexpr (kW8A8) inv = s_inv[xrow];
+        const size_t xbase = (size_t)xrow * a.in_dim;
+        for (uint32_t c = tid; c < a.in_dim; c += kRowsThreads) {
+          float v = x_bits_to_float<XD>(load_x_bits<XD>(a.x, xbase + c));
+          if constexpr (kW8A8) v = qdq_w8a8(v, inv);
+          if ((__float_as_uint(v) & kAbsMask) < kInfBits) continue;
+          for (uint32_t rl = 0; rl < rows; ++rl)
+            atomicOr(&s_kinds[rl],
+                     special_kind(v * iq2xxs_weight_at(a.wb, a.ws, chunk_row0 + rl, c, a.bpr)));
+        }
+        sync();
+        for (uint32_t rl = tid; rl < rows; rl += kRowsThreads) {
+          const uint32_t kinds = s_kinds[rl];
+          float* o = a.out + (size_t)xrow * a.out_dim + chunk_row0 + rl;
+          if (kinds) *o = *o + special_value(kinds);
+        }
+        sync();
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launch policy.
+// ---------------------------------------------------------------------------
+struct RowsPlan {
+  uint32_t rows;  // kRows
+  uint32_t rg_shift, nchunks, grid, slice_shift, nslices, plane_stride;
+  uint32_t xdig_ofs, xsc_ofs, flag_ofs;
+  size_t lds;
+};
+
+static uint32_t align16r(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
+
+// Launch shape for m (2..8) x out_dim x in_dim on num_cus CUs; false when the
+// shape does not fit (31-bit buffer offsets).
+static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, bool vec,
+                      int num_cus, RowsPlan* p) {
+  if (m < 1 || m > 8 || out_dim == 0 || in_dim == 0) return false;
+  const uint64_t bpr = (in_dim + kQK - 1) / kQK;
+  const uint64_t esize = x_dtype == 0 ? 4 : 2;
+  if ((uint64_t)out_dim * bpr * kBytesPerBlock > kOutOfRange - 4096) return false;
+  if ((uint64_t)m * in_dim * esize > kOutOfRange - 4096) return false;
+  p->rows = m <= 4 ? 4 : 8;
+  const uint64_t n_rg = (out_dim + 31) / 32;
+  const uint64_t cus = num_cus > 0 ? (uint64_t)num_cus : 1;
+  uint32_t rs = 0;
+  while (rs < 4 && (n_rg + (1u << rs) - 1) >> rs > cus) ++rs;
+  p->rg_shift = rs;
+  const uint64_t waves_per_rg = kRowsWaves >> rs;
+  p->nchunks = (uint32_t)((n_rg + (1u << rs) - 1) >> rs);
+  p->grid = p->nchunks < cus ? p->nchunks : (uint32_t)cus;
+  // slice: a power of two of super-blocks, at most kU units per wave and two
+  // digitisation tasks per thread
+  const uint64_t units = rows_units((int)p->rows, vec);
+  uint32_t ss = 0;
+  while (2 * (2ull << ss) <= units * waves_per_rg &&
+         (uint64_t)p->rows * (2ull << ss) * 32 <= kRowsMaxTasks * kRowsThreads &&
+         (1ull << ss) < bpr)
+    ++ss;
+  p->slice_shift = ss;
+  const uint64_t S = 1ull << ss;
+  p->nslices = (uint32_t)((bpr + S - 1) / S);
+  p->plane_stride = (uint32_t)(S * kQK + 16);
+  const uint64_t digits = (3ull * p->rows + 1) * p->plane_stride;
+  const uint64_t partials = (uint64_t)kRowsWaves * (p->rows / 2) * 64 * 4;
+  const uint64_t kinds = (1ull << rs) * 32 * 4;
+  uint64_t region = digits > partials ? digits : partials;
+  region = region > kinds ? region : kinds;
+  p->xdig_ofs = RowsTables::kBytes;
+  p->xsc_ofs = p->xdig_ofs + align16r(region);
+  p->flag_ofs = p->xsc_ofs + align16r(S * 8 * p->rows * 4);
+  p->lds = p->flag_ofs + kRowsFlagBytes;
+  return p->lds <= kGemvLdsLimit;
+}
+
+bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
+  RowsPlan p;
+  return plan_rows(m, out_dim, in_dim, x_dtype, false, 1, &p);
+}
+
+template <int XD, bool V, bool Q, int ROWS>
+static hipError_t launch_rows_t(const RowsArgs& a, const RowsPlan& p, hipStream_t stream) {
+  // The tables alone exceed the default 64 KB of dynamic LDS: raise the
+  // limit once per instantiation.
+  static std::atomic<bool> attr_set{false};
+  if (!attr_set.load()) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&iq2xxs_gemv_rows_kernel<XD, V, Q, ROWS>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsLimit);
+    if (e != hipSuccess) return e;
+    attr_set.store(true);
+  }
+  hipLaunchKernelGGL((iq2xxs_gemv_rows_kernel<XD, V, Q, ROWS>), dim3(p.grid),
+                     dim3(kRowsThreads), p.lds, stream, a);
+  return hipGetLastError();
+}
+
+template <int XD, bool V>
+static hipError_t launch_rows_v(const RowsArgs& a, const RowsPlan& p, bool w8a8,
+                                hipStream_t stream) {
+  if (w8a8)
+    return p.rows == 4 ? launch_rows_t<XD, V, true, 4>(a, p, stream)
+                       : launch_rows_t<XD, V, true, 8>(a, p, stream);
+  return p.rows == 4 ? launch_rows_t<XD, V, false, 4>(a, p, stream)
+                     : launch_rows_t<XD, V, false, 8>(a, p, stream);
+}
+
+hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                                   const uint8_t* ws, float* out, uint32_t out_dim,
+                                   uint32_t in_dim, bool w8a8, int num_cus,
+                                   hipStream_t stream) {
+  const size_t esize = x_dtype == 0 ? 4 : 2;
+  const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                   ((size_t)in_dim * esize % 16 == 0);
+  RowsPlan p;
+  if (!plan_rows(m, out_dim, in_dim, x_dtype, vec, num_cus, &p)) return hipErrorInvalidValue;
+  RowsArgs a;
+  a.x = x;
+  a.wb = wb;
+  a.ws = ws;
+  a.out = out;
+  a.m = m;
+  a.out_dim = out_dim;
+  a.in_dim = in_dim;
+  a.bpr = (in_dim + kQK - 1) / kQK;
+  a.n_rg = (out_dim + 31) / 32;
+  a.rg_shift = p.rg_shift;
+  a.nchunks = p.nchunks;
+  a.slice_shift = p.slice_shift;
+  a.nslices = p.nslices;
+  a.wb_records = out_dim * a.bpr * kBytesPerBlock;
+  a.ws_records = out_dim * a.bpr * kScalesPerBlock;
+  a.x_records = m * in_dim * (x_dtype == 0 ? 4u : 2u);
+  a.plane_stride = p.plane_stride;
+  a.xdig_ofs = p.xdig_ofs;
+  a.xsc_ofs = p.xsc_ofs;
+  a.flag_ofs = p.flag_ofs;
+  switch (x_dtype) {
+    case 0: return vec ? launch_rows_v<0, true>(a, p, w8a8, stream)
+                       : launch_rows_v<0, false>(a, p, w8a8, stream);
+    case 1: return vec ? launch_rows_v<1, true>(a, p, w8a8, stream)
+                       : launch_rows_v<1, false>(a, p, w8a8, stream);
+    default: return vec ? launch_rows_v<2, true>(a, p, w8a8, stream)
+                        : launch_rows_v<2, false>(a, p, w8a8, stream);
+  }
+}
+
+}  // namespace cmk

@@ -15,13 +15,19 @@ hipError_t launch_iq2xxs_dequant(const uint8_t* wb, const uint8_t* ws, void* out
                                  uint32_t out_dim, uint32_t in_dim, int num_cus,
                                  hipStream_t stream);
 
-// Decode-shaped matmul (int8-MFMA GEMV), any m; shapes where gemv_supported()
-// holds (K up to about 31000, weights and x below 2 GB).  Needs 16-byte
-// aligned weight_bytes and 2-byte aligned weight_scales.
+// Decode-shaped matmul (int8-MFMA GEMV), any m: the one-row kernel for m = 1,
+// the multi-row kernel on groups of up to 8 rows otherwise; shapes where
+// gemv_supported() holds (m = 1: K up to about 31000; weights and x below
+// 2 GB).  Needs 16-byte aligned weight_bytes and 2-byte aligned weight_scales.
 bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype);
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream);
+// The multi-row kernel alone (1 <= m <= 8).
+bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype);
+hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                                   const uint8_t* ws, float* out, uint32_t out_dim,
+                                   uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream);
 
 // W8A8 per-row inverse scale: inv[r] = 127 / max|x_r| (1 when max < 1e-8).
 hipError_t launch_iq2xxs_row_inv_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
