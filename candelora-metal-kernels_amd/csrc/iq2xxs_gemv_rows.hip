@@ -45,6 +45,11 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr uint32_t kRowsWaves = 16;
 constexpr uint32_t kRowsThreads = kRowsWaves * 64;
 constexpr uint32_t kRowsMaxTasks = 2;  // digitisation tasks per thread and slice
+// Units of the first slice issued before the set-up work (tables, digits); the
+// rest are issued one per computed unit.  A CU's memory pipeline stalls a wave
+// at issue while it is full, so weight requests issued ahead of a barrier
+// would hold every wave at that barrier until they drain.
+constexpr uint32_t kRowsUnitsEarly = 1;
 constexpr uint32_t kRowsFlagBytes = 1024;
 using RowsTables = GemvTables<true>;
 
@@ -238,10 +243,13 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
     row0 = (chunk * R + rgl) * 32;
     const uint32_t code = (!tables_ready && tid < 256) ? kGridCodesDev[tid] : 0u;
     if (tid == 0) *s_special = 0;
-    // set-up loads ahead of the weights: the first slice's activations
+    // set-up loads ahead of the weights: the first slice's activations, then a
+    // barrier (which does not wait for loads), so that every wave's activation
+    // requests are queued before any weight request
     load_x(0);
+    sync();
 #pragma unroll
-    for (uint32_t t = 0; t < kU; ++t) issue_unit(0, t);
+    for (uint32_t t = 0; t < kRowsUnitsEarly && t < kU; ++t) issue_unit(0, t);
     if (!tables_ready) {
       if (tid < 256) {
         store_grid_row<true>(lds, tid, code);
@@ -255,9 +263,11 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
 #pragma unroll
     for (uint32_t t = 0; t < kT; ++t) acc[t] = 0.0f;
 
-    for (uint32_t s = 0; s < a.nslices; ++s) {
-      if (s > 0) load_x(s);  // (the first slice's activations were loaded above)
-      sync();  // the previous slice's digits are consumed (first slice: the flag is clear)
+    // One K slice: digits of slice s (its activations are in flight), then
+    // this wave's units of slice s (each prefetches the next slice's unit).
+    // The first slice runs as straight-line code before the loop, so the wait
+    // for its activations counts exactly the weight loads issued behind them.
+    auto run_slice = [&](uint32_t s) {
       // the zero plane (its area is rewritten by the partial sums at the end)
       if (tid < 16 * S)
         *reinterpret_cast<u32x4*>(xdig + 3 * kRows * a.plane_stride + 16 * tid) =
@@ -268,6 +278,8 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
       const uint32_t s_eff = min(S, a.bpr - sb0);
 #pragma unroll
       for (uint32_t t = 0; t < kU; ++t) {
+        // the first slice's later units: one more in flight per unit computed
+        if (s == 0 && t + kRowsUnitsEarly < kU) issue_unit(0, t + kRowsUnitsEarly);
         const uint32_t ul = wp + P * t;
         if (ul >= 2 * s_eff) break;  // uniform
         // words of the unit's 4 sub-blocks for this lane's row: lane (n, 0)
@@ -326,6 +338,13 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
 #pragma unroll
         for (uint32_t tt = 0; tt < kT; ++tt) acc[tt] = fmaf(au[tt], dq, acc[tt]);
       }
+    };
+    sync();  // tables and the cleared flag
+    run_slice(0);
+    for (uint32_t s = 1; s < a.nslices; ++s) {
+      load_x(s);
+      sync();  // the previous slice's digits are consumed
+      run_slice(s);
     }
 
     // ---- the P waves of a row group add their partial sums in wave order
