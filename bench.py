@@ -341,7 +341,9 @@ def bench_configs(pkg, torch, stream):
 
 def bench_mlp_step(pkg, torch, stream, steps, k=4096, n=14336):
     """One Llama-3-8B MLP decode step with its data dependency: g = gate(x),
-    u = up(x), h = silu(g) * u, y = down(h), over rotated weight copies."""
+    h = silu(g) * up(x), y = down(h), over rotated weight copies; timed with the
+    swiglu step in the up projection's epilogue (three launches) and, for
+    comparison, composed with the swiglu kernel (four launches)."""
     cabi, inputs = pkg.cabi, pkg.inputs
     dev = torch.device("cuda:0")
     sh = int(stream.cuda_stream)
@@ -364,26 +366,40 @@ def bench_mlp_step(pkg, torch, stream, steps, k=4096, n=14336):
                       Matmul(cabi, x, uw, us, u, 1, k, n, cabi.CMK_F32, sh),
                       Matmul(cabi, h, dw, ds, y, 1, n, k, cabi.CMK_F32, sh)))
 
-    def run(i):
+    def run_composed(i):
         gate, up, down = calls[i % copies]
         gate()
         up()
         cabi.swiglu_raw(g.data_ptr(), u.data_ptr(), n, h.data_ptr(), cabi.CMK_F32, sh)
         down()
 
-    for i in range(copies):
-        run(i)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for i in range(steps):
+    def run_fused(i):
+        gate, _, down = calls[i % copies]
+        gate()
+        uw, us = sets[1][i % copies]
+        cabi.matmul_swiglu_raw(x.data_ptr(), cabi.CMK_F32, k, 1, uw.data_ptr(), uw.numel(),
+                               us.data_ptr(), us.numel(), n, k, g.data_ptr(), n, h.data_ptr(), sh)
+        down()
+
+    def timed(run):
+        for i in range(copies):
             run(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    us = replay_timed(torch, cabi, graph, sh, steps, steps) * 1e3 / steps
-    step_bytes = sum(alg_bytes(1, kk, nn) for _, kk, nn in DECODE_SHAPES) + n * 12
-    log(f"[bench] mlp step (gate, up, swiglu, down): {us:.2f} us per step")
-    return {"us_per_step": us, "launches_per_step": 4, "alg_bytes_per_step": step_bytes,
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                run(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        return replay_timed(torch, cabi, graph, sh, steps, steps) * 1e3 / steps
+
+    us_composed = timed(run_composed)
+    us = timed(run_fused)
+    step_bytes = sum(alg_bytes(1, kk, nn) for _, kk, nn in DECODE_SHAPES) + n * 8
+    log(f"[bench] mlp step (gate, up, swiglu, down): {us_composed:.2f} us per step; "
+        f"with silu(g)*u in up's epilogue: {us:.2f} us")
+    return {"us_per_step": us, "launches_per_step": 3, "us_per_step_composed": us_composed,
+            "launches_per_step_composed": 4, "alg_bytes_per_step": step_bytes,
             "gbs": step_bytes / (us * 1e-6) / 1e9, "steps": steps}
 
 

@@ -5,7 +5,8 @@ include/cmk_iq2.h).  This package gives Python callers the same surface as the
 reference crate's public API (iq2_matmul, iq2_matmul_with_activation_quant,
 iq2_dequantize_to_f16, Iq2MatmulVariant, ActivationQuantMode/Config) over
 PyTorch device tensors, plus the GGUF block split (iq2_split_gguf_blocks), the MLP's
-silu(gate) * up step (swiglu) and seeded input generators.
+silu(gate) * up step (swiglu, and iq2_matmul_swiglu: the step folded into the
+up projection's epilogue) and seeded input generators.
 """
 
 from . import cabi, inputs  # noqa: F401
@@ -18,6 +19,7 @@ from .iq2_matmul import (  # noqa: F401
     iq2_matmul_with_activation_quant,
     iq2_s_matmul,
     iq2_split_gguf_blocks,
+    iq2_matmul_swiglu,
     iq2_xs_matmul,
     iq2_xxs_matmul,
     iq3_s_matmul,
@@ -37,5 +39,6 @@ __all__ = [
     "iq2_s_matmul",
     "iq3_s_matmul",
     "iq2_split_gguf_blocks",
+    "iq2_matmul_swiglu",
     "swiglu",
 ]

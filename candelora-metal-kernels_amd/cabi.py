@@ -32,6 +32,7 @@ EXPORTED = (
     "cmk_iq2_dequantize",
     "cmk_iq2_split_gguf_blocks",
     "cmk_swiglu",
+    "cmk_iq2_matmul_swiglu",
     "cmk_last_error",
     "cmk_abi_version",
     "cmk_iq2_matmul_path",
@@ -86,6 +87,8 @@ def lib() -> ctypes.CDLL:
     L.cmk_iq2_split_gguf_blocks.restype = I
     L.cmk_swiglu.argtypes = [P, P, S, I, P, P]
     L.cmk_swiglu.restype = I
+    L.cmk_iq2_matmul_swiglu.argtypes = [P, I, S, S, P, S, P, S, S, S, P, S, P, P]
+    L.cmk_iq2_matmul_swiglu.restype = I
     L.cmk_iq2_dequantize.restype = I
     L.cmk_last_error.argtypes = []
     L.cmk_last_error.restype = ctypes.c_char_p
@@ -158,6 +161,12 @@ def split_gguf_raw(blocks_ptr, blocks_len, n_blocks, variant, wb_ptr, wb_len, ws
 
 def swiglu_raw(gate_ptr, up_ptr, n, out_ptr, out_dtype=CMK_F32, stream=None) -> None:
     check(lib().cmk_swiglu(gate_ptr, up_ptr, n, out_dtype, out_ptr, stream))
+
+
+def matmul_swiglu_raw(x_ptr, x_dtype, x_len, m, wb_ptr, wb_len, ws_ptr, ws_len, out_dim, in_dim,
+                      gate_ptr, gate_len, out_ptr, stream=None) -> None:
+    check(lib().cmk_iq2_matmul_swiglu(x_ptr, x_dtype, x_len, m, wb_ptr, wb_len, ws_ptr, ws_len,
+                                      out_dim, in_dim, gate_ptr, gate_len, out_ptr, stream))
 
 
 def dequantize_raw(wb_ptr, wb_len, ws_ptr, ws_len, out_dim, in_dim, out_ptr,

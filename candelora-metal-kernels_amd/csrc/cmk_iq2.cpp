@@ -477,6 +477,52 @@ int cmk_swiglu(const float* gate, const float* up, size_t n, cmk_dtype out_dtype
   return ok();
 }
 
+int cmk_iq2_matmul_swiglu(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
+                          const uint8_t* weight_bytes, size_t weight_bytes_len,
+                          const uint8_t* weight_scales, size_t weight_scales_len,
+                          size_t out_dim, size_t in_dim, const float* gate, size_t gate_len,
+                          float* out, void* stream) {
+  int md = CMK_ACT_QUANT_OFF;
+  Dims dims;
+  int rc = validate_matmul((int)x_dtype, m, out_dim, in_dim, CMK_IQ2_XXS, &md, 0,
+                           weight_bytes_len, weight_scales_len, true, &dims);
+  if (rc != CMK_OK) return rc;
+  if (m == 0) return ok();
+  size_t need_x, need_out;
+  if (!checked_mul(m, in_dim, &need_x) || !checked_mul(m, out_dim, &need_out))
+    return fail(CMK_ERR_INVALID_ARGUMENT, "matmul_swiglu size overflow");
+  if (x_len < need_x)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "matmul_swiglu x too small: got %zu expected at least %zu", x_len, need_x);
+  if (gate_len < need_out)
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "matmul_swiglu gate too small: got %zu expected at least %zu", gate_len,
+                need_out);
+  if (!x || !weight_bytes || !weight_scales || !gate || !out)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "matmul_swiglu null pointer argument");
+  const size_t esize = x_dtype == CMK_F32 ? 4 : 2;
+  if (!aligned(x, esize) || !aligned(gate, 4) || !aligned(out, 4))
+    return fail(CMK_ERR_INVALID_ARGUMENT,
+                "matmul_swiglu x, gate and out must be aligned to their element size");
+  const uintptr_t g0 = reinterpret_cast<uintptr_t>(gate), o0 = reinterpret_cast<uintptr_t>(out);
+  if (g0 < o0 + need_out * 4 && o0 < g0 + need_out * 4)
+    return fail(CMK_ERR_INVALID_ARGUMENT, "matmul_swiglu gate must not overlap out");
+  if (choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x, weight_bytes, weight_scales) !=
+      Path::Gemv)
+    return fail(CMK_ERR_UNSUPPORTED,
+                "matmul_swiglu serves the decode-shaped kernels (m <= %zu for F32 x, <= %zu for "
+                "F16/BF16, aligned weights): use cmk_iq2_matmul and cmk_swiglu",
+                kGemvMaxMF32, kGemvMaxM);
+  int cus = 0;
+  rc = current_cu_count(&cus);
+  if (rc != CMK_OK) return rc;
+  const hipError_t e = cmk::launch_iq2xxs_gemv(x, (int)x_dtype, dims.m, weight_bytes,
+                                               weight_scales, out, dims.out_dim, dims.in_dim,
+                                               false, cus, static_cast<hipStream_t>(stream), gate);
+  if (e != hipSuccess) return hip_fail(e, "matmul_swiglu launch");
+  return ok();
+}
+
 // ---- runtime wrappers -----------------------------------------------------
 
 int cmk_device_count(int* count) {

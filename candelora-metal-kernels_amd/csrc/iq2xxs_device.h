@@ -94,6 +94,15 @@ __device__ __forceinline__ float x_bits_to_float(uint32_t b) {
     return bf16_bits_to_float((uint16_t)b);
 }
 
+// silu(g) * u = g / (1 + exp(-g)) * u in fp32: the step between a gated MLP's
+// gate/up and down projections.  The swiglu kernel and the matmul epilogues
+// that fold the step in evaluate this same expression, so both routes give the
+// same bits.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return (g / (1.0f + expf(-g))) * u;
+}
+
+
 // Eight consecutive activations x[base + c0 .. +8) as raw bits.  A task that
 // is out of range issues no load at all (its registers stay undefined) and
 // in-range elements are never selected right after the load: the validity

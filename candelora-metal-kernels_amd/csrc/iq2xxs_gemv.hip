@@ -151,6 +151,9 @@ struct GemvArgs {
   uint32_t plane_stride;  // LDS bytes between the three digit planes
   uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs, flag_ofs;  // LDS layout
   int w8a8;
+  // Non-null: out = silu(gate) * (x . w), the gated MLP step in the epilogue
+  // (gate: [m, out_dim] f32, the gate projection's output).
+  const float* gate;
 };
 
 // XD: activation dtype (0 f32, 1 f16, 2 bf16); kVecX: activations can be read
@@ -535,13 +538,25 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     }
     sync();
     const bool special = *s_special == gen;  // uniform
+    const bool gated = a.gate != nullptr && !special;
     for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
       const float* p = red + (rl >> 2) * a.nslices * 4 + (rl & 3);
       float sum = 0.0f;
       for (uint32_t sl = 0; sl < a.nslices; ++sl) sum += p[sl * 4];
-      a.out[(size_t)mrow * a.out_dim + row_begin + rl] = sum;
+      const size_t o = (size_t)mrow * a.out_dim + row_begin + rl;
+      a.out[o] = gated ? silu_mul(a.gate[o], sum) : sum;
     }
-    if (special) fix_up_special(mrow);
+    if (special) {
+      fix_up_special(mrow);
+      // the gated step on the completed sums (each thread rereads the rows
+      // it wrote)
+      if (a.gate != nullptr) {
+        for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
+          const size_t o = (size_t)mrow * a.out_dim + row_begin + rl;
+          a.out[o] = silu_mul(a.gate[o], a.out[o]);
+        }
+      }
+    }
   };
 
   // ======== first chunk (straight-line) ========
@@ -735,7 +750,7 @@ static hipError_t launch_gemv_v(const GemvArgs& a, const GemvPlan& p, bool vec,
 
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              bool w8a8, int num_cus, hipStream_t stream) {
+                              bool w8a8, int num_cus, hipStream_t stream, const float* gate) {
   if (m > 1) {
     // groups of up to 8 activation rows, each decoding the weights once
     const size_t esize = x_dtype == 0 ? 4 : 2;
@@ -743,7 +758,7 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
       const hipError_t e = launch_iq2xxs_gemv_rows(
           static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize, x_dtype,
           m - r0 < 8 ? m - r0 : 8, wb, ws, out + (size_t)r0 * out_dim, out_dim, in_dim, w8a8,
-          num_cus, stream);
+          num_cus, stream, gate ? gate + (size_t)r0 * out_dim : nullptr);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -778,6 +793,7 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
   a.wred_ofs = p.wred_ofs;
   a.flag_ofs = p.flag_ofs;
   a.w8a8 = w8a8 ? 1 : 0;
+  a.gate = gate;
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                    ((size_t)in_dim * esize % 16 == 0);

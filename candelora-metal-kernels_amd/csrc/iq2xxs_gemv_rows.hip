@@ -67,6 +67,9 @@ struct RowsArgs {
   uint32_t wb_records, ws_records, x_records;  // bytes addressable by the buffer loads
   uint32_t plane_stride;                       // LDS bytes between digit planes
   uint32_t xdig_ofs, xsc_ofs, flag_ofs;        // LDS layout; partial sums reuse xdig
+  // Non-null: out = silu(gate) * (x . w), the gated MLP step in the epilogue
+  // (gate: [m, out_dim] f32, the gate projection's output).
+  const float* gate;
 };
 
 // Units a wave holds per slice: four for up to 4 rows read as vectors, two
@@ -353,18 +356,22 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
     for (uint32_t tt = 0; tt < kT; ++tt) red[((rgl * P + wp) * kT + tt) * 64 + lane] = acc[tt];
     sync();
     const uint32_t chunk_row0 = chunk * R * 32;
+    const uint32_t special = *s_special;  // uniform (final since the last digitisation)
+    const bool gated = a.gate != nullptr && special == 0;
     for (uint32_t o = tid; o < R * kT * 64; o += kRowsThreads) {
       const uint32_t ol = o & 63, tt = (o >> 6) % kT, rg = (o >> 6) / kT;
       float sum = 0.0f;
       for (uint32_t w = 0; w < P; ++w) sum += red[((rg * P + w) * kT + tt) * 64 + ol];
       const uint32_t xrow = 2 * tt + (ol >> 5), row = chunk_row0 + rg * 32 + (ol & 31);
-      if (xrow < a.m && row < a.out_dim) a.out[(size_t)xrow * a.out_dim + row] = sum;
+      if (xrow < a.m && row < a.out_dim) {
+        const size_t i = (size_t)xrow * a.out_dim + row;
+        a.out[i] = gated ? silu_mul(a.gate[i], sum) : sum;
+      }
     }
 
     // ---- rows that held a NaN or an infinity: add the kind of the
     // set-aside terms x_c * w_rc to the chunk's outputs
     sync();
-    const uint32_t special = *s_special;  // uniform
     if (special) {
       const uint32_t rows = min(R * 32, a.out_dim - min(chunk_row0, a.out_dim));
       for (uint32_t xrow = 0; xrow < a.m; ++xrow) {
@@ -389,6 +396,15 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
           if (kinds) *o = *o + special_value(kinds);
         }
         sync();
+      }
+      // the gated step on the completed sums
+      if (a.gate != nullptr) {
+        const uint32_t rows = min(R * 32, a.out_dim - min(chunk_row0, a.out_dim));
+        for (uint32_t i = tid; i < a.m * rows; i += kRowsThreads) {
+          const uint32_t xrow = i / rows, rl = i - xrow * rows;
+          const size_t o = (size_t)xrow * a.out_dim + chunk_row0 + rl;
+          a.out[o] = silu_mul(a.gate[o], a.out[o]);
+        }
       }
     }
   }
@@ -482,8 +498,8 @@ static hipError_t launch_rows_v(const RowsArgs& a, const RowsPlan& p, bool w8a8,
 
 hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                    const uint8_t* ws, float* out, uint32_t out_dim,
-                                   uint32_t in_dim, bool w8a8, int num_cus,
-                                   hipStream_t stream) {
+                                   uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
+                                   const float* gate) {
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                    ((size_t)in_dim * esize % 16 == 0);
@@ -510,6 +526,7 @@ hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const
   a.xdig_ofs = p.xdig_ofs;
   a.xsc_ofs = p.xsc_ofs;
   a.flag_ofs = p.flag_ofs;
+  a.gate = gate;
   switch (x_dtype) {
     case 0: return vec ? launch_rows_v<0, true>(a, p, w8a8, stream)
                        : launch_rows_v<0, false>(a, p, w8a8, stream);

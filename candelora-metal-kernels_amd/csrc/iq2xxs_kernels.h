@@ -19,15 +19,19 @@ hipError_t launch_iq2xxs_dequant(const uint8_t* wb, const uint8_t* ws, void* out
 // the multi-row kernel on groups of up to 8 rows otherwise; shapes where
 // gemv_supported() holds (m = 1: K up to about 31000; weights and x below
 // 2 GB).  Needs 16-byte aligned weight_bytes and 2-byte aligned weight_scales.
+// gate non-null: out = silu(gate) * (x . w) with gate [m, out_dim] f32 (not
+// overlapping out), the gated MLP step in the epilogue.
 bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype);
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              bool w8a8, int num_cus, hipStream_t stream);
+                              bool w8a8, int num_cus, hipStream_t stream,
+                              const float* gate = nullptr);
 // The multi-row kernel alone (1 <= m <= 8).
 bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype);
 hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                    const uint8_t* ws, float* out, uint32_t out_dim,
-                                   uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream);
+                                   uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
+                                   const float* gate = nullptr);
 
 // W8A8 per-row inverse scale: inv[r] = 127 / max|x_r| (1 when max < 1e-8).
 hipError_t launch_iq2xxs_row_inv_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,

@@ -17,10 +17,6 @@
 
 namespace cmk {
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  return (g / (1.0f + expf(-g))) * u;
-}
-
 __device__ __forceinline__ uint16_t mlp_f16_rne(float v) {
   return __half_as_ushort(__float2half_rn(v));
 }

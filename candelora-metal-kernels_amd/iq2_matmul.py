@@ -197,6 +197,37 @@ def swiglu(gate, up, out_dtype=torch.float32):
     return out
 
 
+def iq2_matmul_swiglu(x, weight_bytes, weight_scales, out_dim, in_dim, gate):
+    """silu(gate) * iq2_xxs_matmul(x, ...): the up projection of a gated MLP
+    with the swiglu step in its epilogue, so the step needs no launch of its
+    own.  Equal, bit for bit, to swiglu(gate, iq2_xxs_matmul(x, ...)).  gate is
+    F32 shaped like the output ([out_dim] or [m, out_dim]); m <= 16 for F32 x,
+    <= 8 for F16 / BF16.  No counterpart in the reference, whose callers
+    compose the MLP from candle ops."""
+    if x.device.type != "cuda" or gate.device != x.device:
+        raise Iq2MatmulError("matmul_swiglu requires x and gate on one HIP device")
+    if weight_bytes.device != x.device or weight_scales.device != x.device:
+        raise Iq2MatmulError("matmul_swiglu requires the weights on the device of x")
+    _check_weights("matmul_swiglu", x, weight_bytes, weight_scales)
+    x2, m, squeeze = _parse_x_shape(x, in_dim)
+    x2 = x2.contiguous()
+    if x2.dtype not in _DTYPES:
+        raise Iq2MatmulError(f"iq2_matmul unsupported x dtype: {_dtype_name(x2.dtype)}")
+    if gate.dtype != torch.float32 or gate.numel() != m * out_dim:
+        raise Iq2MatmulError("matmul_swiglu expects an F32 gate shaped like the output")
+    g = gate.contiguous()
+    out = torch.empty((m, out_dim), dtype=torch.float32, device=x.device)
+    if m > 0:
+        try:
+            cabi.matmul_swiglu_raw(x2.data_ptr(), _DTYPES[x2.dtype], x2.numel(), m,
+                                   weight_bytes.data_ptr(), weight_bytes.numel(),
+                                   weight_scales.data_ptr(), weight_scales.numel(), out_dim,
+                                   in_dim, g.data_ptr(), g.numel(), out.data_ptr(), _stream(x))
+        except cabi.CmkError as e:
+            raise Iq2MatmulError(str(e)) from None
+    return out.squeeze(0) if squeeze else out
+
+
 def iq2_xxs_matmul(x, weight_bytes, weight_scales, out_dim, in_dim):
     return iq2_matmul(x, weight_bytes, weight_scales, out_dim, in_dim, Iq2MatmulVariant.Iq2Xxs)
 

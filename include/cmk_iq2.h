@@ -179,6 +179,25 @@ int cmk_iq2_split_gguf_blocks(const uint8_t *blocks, size_t blocks_len, size_t n
 int cmk_swiglu(const float *gate, const float *up, size_t n, cmk_dtype out_dtype, void *out,
                void *stream);
 
+/*
+ * The up projection of a gated MLP with the step above folded into its
+ * epilogue: out[m, out_dim] = silu(gate) * iq2_matmul(x) for the IQ2_XXS
+ * weights, elementwise, with gate the gate projection's output ([m, out_dim]
+ * f32, `gate_len` elements, not overlapping out).  Equal, bit for bit, to
+ * cmk_iq2_matmul into a buffer u followed by cmk_swiglu(gate, u, F32): the
+ * epilogue evaluates the same fp32 expression on the same sum.  Serves the
+ * decode-shaped kernels only (m <= 16 for F32 x, m <= 8 for F16 / BF16, no
+ * activation quantisation, weight_bytes 16-byte and weight_scales 2-byte
+ * aligned); CMK_ERR_UNSUPPORTED otherwise.  No workspace.  No counterpart in
+ * the reference, whose callers compose the MLP from candle ops.  Device
+ * pointers, asynchronous on `stream`.
+ */
+int cmk_iq2_matmul_swiglu(const void *x, cmk_dtype x_dtype, size_t x_len, size_t m,
+                          const uint8_t *weight_bytes, size_t weight_bytes_len,
+                          const uint8_t *weight_scales, size_t weight_scales_len,
+                          size_t out_dim, size_t in_dim, const float *gate, size_t gate_len,
+                          float *out, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* Errors and introspection                                                  */
 /* ------------------------------------------------------------------------ */

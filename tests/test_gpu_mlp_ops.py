@@ -98,3 +98,54 @@ def test_mlp_chain_against_oracle(pkg, oracle, inputs, dev):
     assert np.max(err / np.maximum(scale, 1e-30)) <= 1e-4
     big = np.abs(y64) >= 1e-2 * np.abs(y64).max()
     assert np.max(err[big] / np.abs(y64[big])) <= 1e-3
+
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("m", [1, 3, 8, 13])
+@pytest.mark.parametrize("k,n", [(4096, 14336), (14336, 512), (1000, 300)])
+def test_matmul_swiglu_equals_matmul_then_swiglu(pkg, inputs, dev, m, k, n, dtype):
+    """The up projection with silu(gate) * u in its epilogue gives the same
+    bits as the matmul followed by cmk_swiglu (one fp32 expression on the same
+    sums)."""
+    if dtype == torch.float16 and m > 8:
+        pytest.skip("f16 x above 8 rows takes the MFMA GEMM")
+    wu, su = inputs.synthetic_weights(n, k, seed=21)
+    x = torch.from_numpy(inputs.synthetic_x(m, k, seed=22)).to(dev).to(dtype)
+    gate = torch.from_numpy(inputs.synthetic_x(m, n, seed=23)).to(dev)
+    wut, sut = torch.from_numpy(wu).to(dev), torch.from_numpy(su).to(dev)
+    ref = pkg.swiglu(gate, pkg.iq2_xxs_matmul(x, wut, sut, n, k))
+    got = pkg.iq2_matmul_swiglu(x, wut, sut, n, k, gate)
+    assert torch.equal(ref, got)
+    if m == 1:  # rank-1 x and gate give a rank-1 output
+        got1 = pkg.iq2_matmul_swiglu(x[0], wut, sut, n, k, gate[0])
+        assert got1.shape == (n,) and torch.equal(got1, ref[0])
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_matmul_swiglu_nonfinite(pkg, inputs, dev, m):
+    """A NaN activation (the set-aside fix-up path) and a NaN / infinite gate
+    reach the output as through the matmul then swiglu."""
+    k, n = 4096, 1024
+    wu, su = inputs.synthetic_weights(n, k, seed=31)
+    wut, sut = torch.from_numpy(wu).to(dev), torch.from_numpy(su).to(dev)
+    x = torch.from_numpy(inputs.synthetic_x(m, k, seed=32)).to(dev)
+    x[m - 1, 77] = float("inf")
+    gate = torch.from_numpy(inputs.synthetic_x(m, n, seed=33)).to(dev)
+    gate[0, 5] = float("nan")
+    gate[0, 6] = -float("inf")
+    ref = pkg.swiglu(gate, pkg.iq2_xxs_matmul(x, wut, sut, n, k))
+    got = pkg.iq2_matmul_swiglu(x, wut, sut, n, k, gate)
+    assert torch.equal(torch.isnan(ref), torch.isnan(got))
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(got))
+    assert torch.equal(ref[fin], got[fin])
+
+
+def test_matmul_swiglu_rejects_gemm_shapes(pkg, inputs, dev):
+    wu, su = inputs.synthetic_weights(64, 256)
+    x = torch.zeros((17, 256), dtype=torch.float32, device=dev)
+    gate = torch.zeros((17, 64), dtype=torch.float32, device=dev)
+    with pytest.raises(pkg.Iq2MatmulError, match="decode-shaped"):
+        pkg.iq2_matmul_swiglu(x, torch.from_numpy(wu).to(dev), torch.from_numpy(su).to(dev), 64,
+                              256, gate)
