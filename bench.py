@@ -184,6 +184,53 @@ def bench_decode(pkg, torch, stream, steps, warmup):
     }
 
 
+def bench_read_floor(pkg, torch, stream, steps):
+    """The plain-read floor beside the decode line: libcmk_probe.so's kernel
+    reading the bytes of one decode launch (the mean of the three launches'
+    algorithmic bytes, 16-byte loads, no decoding) from rotated buffers, timed
+    like the decode line (one graph of `steps` launches, events around a
+    replay that follows untimed ones)."""
+    import ctypes
+    cabi = pkg.cabi
+    path = os.path.join(os.path.dirname(cabi.LIB_PATH), "libcmk_probe.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build with __graft_entry__.build()")
+    probe = ctypes.CDLL(path)
+    probe.cmk_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_void_p]
+    probe.cmk_probe_read.restype = ctypes.c_int
+    dev = torch.device("cuda:0")
+    sh = int(stream.cuda_stream)
+    nbytes = sum(alg_bytes(1, k, n) for _, k, n in DECODE_SHAPES) // len(DECODE_SHAPES)
+    nbytes = (nbytes + 15) // 16 * 16
+    copies = max(2, math.ceil(2 * MALL_BYTES / nbytes))
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(copies)]
+    blocks = 4096
+    sink = torch.zeros(blocks, dtype=torch.int32, device=dev)
+
+    def run(i):
+        rc = probe.cmk_probe_read(bufs[i % copies].data_ptr(), nbytes, sink.data_ptr(), blocks,
+                                  sh)
+        if rc != 0:
+            raise RuntimeError(f"cmk_probe_read failed: hip error {rc}")
+
+    for i in range(copies):
+        run(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            run(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    us = replay_timed(torch, cabi, graph, sh, steps, DECODE_WARM_STEPS) * 1e3 / steps
+    log(f"[bench] read floor: {nbytes/1e6:.2f} MB in {us:.2f} us per launch "
+        f"({nbytes / (us * 1e-6) / 1e9:.1f} GB/s)")
+    return {"bytes": nbytes, "us_per_launch": us, "gbs": nbytes / (us * 1e-6) / 1e9,
+            "kernel": "probe_read_kernel (libcmk_probe.so; 4096 x 256 threads, 16-byte "
+                      "nontemporal loads)", "launches": steps}
+
+
 def bench_prefill(pkg, torch, stream, steps, warmup, m=512, k=4096, n=14336):
     cabi, inputs = pkg.cabi, pkg.inputs
     dev = torch.device("cuda:0")
@@ -540,6 +587,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (for rocprof counter calibration)")
+    ap.add_argument("--only", choices=["decode", "prefill", "read-floor"],
+                    help="time one line only and print it (for profiling runs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -570,8 +619,20 @@ def main():
     props = pkg.cabi.device_props()
     log(f"[bench] device: {props}")
     stream = torch.cuda.Stream()  # default priority
+    if args.only:
+        with torch.cuda.stream(stream):
+            if args.only == "decode":
+                res = bench_decode(pkg, torch, stream, args.steps, args.warmup)
+            elif args.only == "prefill":
+                res = bench_prefill(pkg, torch, stream, args.prefill_steps, 5)
+            else:
+                res = bench_read_floor(pkg, torch, stream, args.steps * len(DECODE_SHAPES))
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, **res}))
+        return
     with torch.cuda.stream(stream):
         dec = bench_decode(pkg, torch, stream, args.steps, args.warmup)
+        floor = bench_read_floor(pkg, torch, stream, args.steps * len(DECODE_SHAPES))
         prefill = (None if args.no_prefill
                    else bench_prefill(pkg, torch, stream, args.prefill_steps, 5))
         variants = (None if args.no_variants
@@ -613,7 +674,8 @@ def main():
                      "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false> "
                                "(XT = 1 for K=4096, 2 for K=14336)",
                      "mean_launch_us": dec["mean_launch_us"],
-                     "alg_bytes_per_launch": dec["per_launch_bytes"]},
+                     "alg_bytes_per_launch": dec["per_launch_bytes"],
+                     "read_floor": floor},
     }
     if prefill is not None:
         line["prefill_m512"] = prefill

@@ -6,6 +6,7 @@ candelora-metal-kernels_amd/_build/, the shared libraries next to this file.
 
   libcmk_iq2.so        C ABI (include/cmk_iq2.h): kernels + dispatch + runtime wrappers
   libcandelora_iq2.so  C++ host layer with the reference's API (host/), linked to libcmk_iq2
+  libcmk_probe.so      bench.py's plain HBM read (the floor the decode GEMV is set beside)
 """
 
 from __future__ import annotations
@@ -25,6 +26,7 @@ INCLUDE = os.path.join(REPO, "include")
 
 LIB = os.path.join(PKG, "libcmk_iq2.so")
 HOST_LIB = os.path.join(PKG, "libcandelora_iq2.so")
+PROBE_LIB = os.path.join(PKG, "libcmk_probe.so")
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -83,6 +85,15 @@ def build_lib() -> str:
     return LIB
 
 
+def build_probe() -> str:
+    """bench.py's plain-read kernel (csrc/probe_read.hip), a library of its own."""
+    obj = _compile(os.path.join(CSRC, "probe_read.hip"))
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, obj])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 def build_host() -> str:
     """C++ host layer with the reference API (host code only, over the C ABI)."""
     host_src = os.path.join(HOST, "iq2_matmul.cpp")
@@ -102,12 +113,13 @@ def build() -> str:
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     lib = build_lib()
     build_host()
+    build_probe()
     return lib
 
 
 def clean() -> None:
     shutil.rmtree(OBJ, ignore_errors=True)
-    for p in (LIB, HOST_LIB):
+    for p in (LIB, HOST_LIB, PROBE_LIB):
         if os.path.exists(p):
             os.remove(p)
 
