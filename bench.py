@@ -260,8 +260,10 @@ def bench_prefill(pkg, torch, stream, steps, warmup, m=512, k=4096, n=14336):
             "gbs": alg_bytes(m, k, n, 2) / t / 1e9, "steps": steps}
 
 
-# IQ2_XS, IQ2_S, IQ3_S: (ABI variant, bytes, scales per 256-weight block)
-VARIANTS = [("iq2_xs", 1, 64, 10), ("iq2_s", 2, 72, 10), ("iq3_s", 3, 104, 6)]
+# IQ2_XS, IQ2_S, IQ3_S: (ABI variant, bytes, scales per 256-weight block, the
+# format policy of the multi-row decode kernel that serves them)
+VARIANTS = [("iq2_xs", 1, 64, 10, "RowsFmtXS"), ("iq2_s", 2, 72, 10, "RowsFmtS"),
+            ("iq3_s", 3, 104, 6, "RowsFmtS3")]
 
 
 def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
@@ -274,7 +276,7 @@ def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
     x = torch.from_numpy(inputs.synthetic_x(1, k)).to(dev)
     out = torch.empty((1, n), dtype=torch.float32, device=dev)
     res = {}
-    for name, v, bpb, spb in VARIANTS:
+    for name, v, bpb, spb, fmt in VARIANTS:
         rng = np.random.default_rng(v)
         wb = rng.integers(0, 256, n * bpr * bpb, dtype=np.uint8)
         ws = rng.integers(0, 256, n * bpr * spb, dtype=np.uint8)
@@ -298,7 +300,8 @@ def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
         res[name] = {"k": k, "n": n, "m": 1, "mean_launch_us": us, "alg_bytes_per_launch": alg,
                      "gbs": alg / (us * 1e-6) / 1e9,
                      "frac_of_hbm_peak": alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                     "kernel": f"cmk::iq_variant_matmul_kernel<{v}>", "launches": steps}
+                     "kernel": f"cmk::iq_gemv_rows_kernel<cmk::{fmt}, 0, true, false, 4>",
+                     "launches": steps}
         log(f"[bench] {name}: {us:.2f} us per launch, {res[name]['gbs']:.1f} GB/s")
         del graph, calls, reps
     return res

@@ -311,7 +311,13 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   float* partials =
       need_ws > head_ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + head_ws)
                         : nullptr;
-  if (row_inv && w8a8) {  // (f32 rows staged for the GEMM get their scales there)
+  // IQ2_XS / IQ2_S / IQ3_S with aligned weights: the multi-row decode kernel
+  // (W8A8 scales computed there; the workspace stays unused)
+  const bool variant_rows = p == Path::Variant && aligned(weight_bytes, 16) &&
+                            aligned(weight_scales, 2) &&
+                            cmk::variant_rows_supported((int)variant, dims.out_dim, dims.in_dim,
+                                                        (int)x_dtype);
+  if (row_inv && w8a8 && !variant_rows) {  // (f32 rows staged for the GEMM get their scales there)
     e = cmk::launch_iq2xxs_row_inv_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s);
     if (e != hipSuccess) return hip_fail(e, "iq2_matmul row scale launch");
   }
@@ -331,9 +337,13 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
                                            out, dims.out_dim, dims.in_dim, row_inv, cus, s);
       break;
     case Path::Variant:
-      e = cmk::launch_iq_variant_matmul((int)variant, x, (int)x_dtype, dims.m, weight_bytes,
-                                        weight_scales, out, dims.out_dim, dims.in_dim, row_inv,
-                                        cus, s);
+      e = variant_rows
+              ? cmk::launch_iq_variant_rows((int)variant, x, (int)x_dtype, dims.m, weight_bytes,
+                                            weight_scales, out, dims.out_dim, dims.in_dim, w8a8,
+                                            cus, s)
+              : cmk::launch_iq_variant_matmul((int)variant, x, (int)x_dtype, dims.m,
+                                              weight_bytes, weight_scales, out, dims.out_dim,
+                                              dims.in_dim, row_inv, cus, s);
       break;
   }
   if (e != hipSuccess) return hip_fail(e, "iq2_matmul launch");

@@ -1,14 +1,22 @@
-// iq2xxs_gemv_rows.hip — IQ2_XXS matmul for 2..8 activation rows on gfx950.
+// iq2xxs_gemv_rows.hip — IQ2_XXS matmul for 2..8 activation rows, and IQ2_XS,
+// IQ2_S and IQ3_S matmuls for up to 8 rows per launch, on gfx950.
 //
 // Replaces iq2_xxs_matmul_kernel / iq2_xxs_matmul_w8a8_kernel
-// (src/metal_src/iq2_matmul.metal:188-240, 436-499) for small m > 1.  The
-// reference runs one thread per output, so every weight is decoded once per
-// activation row; here a weight is decoded once per launch and one MFMA
-// multiplies it against all the rows.
+// (src/metal_src/iq2_matmul.metal:188-240, 436-499) for small m > 1, and the
+// IQ2_XS / IQ2_S / IQ3_S matmul kernels (:242-434, 501-699) for m <= 8 per
+// launch.  The reference runs one thread per output, so every weight is
+// decoded once per activation row; here a weight is decoded once per launch
+// and one MFMA multiplies it against all the rows.  What differs between the
+// formats (tables, loads, code expansion, sub-scales) is a policy class from
+// iq_rows_formats.h; formats whose sub-scale covers 16 weights (IQ2_XS, IQ2_S)
+// take two v_mfma_i32_32x32x16_i8 per sub-block instead of one
+// v_mfma_i32_32x32x32_i8, with lane l supplying columns 8 (l/32) .. + 7 of
+// each 16-column half.
 //
 // Arithmetic.  The activations become the same exact integer digits as in the
 // one-row kernel (iq2xxs_gemv.hip): per 32-column sub-block, three signed 8-bit
-// planes of rint(x * 2^(20-e)), in LDS.  The codes expand through the same
+// planes of rint(x * 2^(D-e)), in LDS (D = 20 bits for IQ2_XXS, 21 for the
+// formats whose plane sums leave room for it).  The codes expand through the same
 // LDS tables ({g, -g} codebook rows, 8-byte sign masks, one bit select per
 // dword).  v_mfma_i32_32x32x32_i8 then takes
 //   A: 32 rows = 8 activation rows x 4 digit planes (plane 3 and absent rows
@@ -19,7 +27,7 @@
 // the hardware's byte order is), and receives C rows 8*(r/4) + 4*(l/32) + r%4
 // in register r: planes 0..2 of activation rows 2t + l/32 (t = r/4) against
 // weight row l%32.  The three plane sums combine exactly in int32; the scale
-// (2s+1) * 2^(e-23) is applied in fp32 per sub-block, d once per super-block.
+// (2s+1) * 2^(e-D-3) is applied in fp32 per sub-block, d once per super-block.
 //
 // Work split.  A *unit* is 32 weight rows x half a super-block (4 sub-blocks,
 // 1 KB of codes: one 16-byte load per lane).  A workgroup of 16 waves owns a
@@ -37,6 +45,7 @@
 #include "iq2xxs_device.h"
 #include "iq2xxs_gemv_common.h"
 #include "iq2xxs_kernels.h"
+#include "iq_rows_formats.h"
 
 namespace cmk {
 
@@ -51,7 +60,6 @@ constexpr uint32_t kRowsMaxTasks = 2;  // digitisation tasks per thread and slic
 // would hold every wave at that barrier until they drain.
 constexpr uint32_t kRowsUnitsEarly = 1;
 constexpr uint32_t kRowsFlagBytes = 1024;
-using RowsTables = GemvTables<true>;
 
 struct RowsArgs {
   const void* x;
@@ -72,18 +80,22 @@ struct RowsArgs {
   const float* gate;
 };
 
-// Units a wave holds per slice: four for up to 4 rows read as vectors, two
-// otherwise (the registers a 1024-thread workgroup leaves a wave: 128).
-constexpr uint32_t rows_units(int rows, bool vec) { return rows == 4 && vec ? 4 : 2; }
+// Units a wave holds per slice: four for up to 4 rows read as vectors with
+// IQ2_XXS's 5-register units, two otherwise (the registers a 1024-thread
+// workgroup leaves a wave: 128).
+template <class F>
+constexpr uint32_t rows_units(int rows, bool vec) {
+  return rows == 4 && vec && sizeof(typename F::Unit) <= 20 ? 4 : 2;
+}
 
-// XD: activation dtype (0 f32, 1 f16, 2 bf16); kVecX: activations can be read
-// as aligned 16-byte vectors; kW8A8: fake-quantise x per row first; kRows: 4
-// or 8, at least m.
-template <int XD, bool kVecX, bool kW8A8, int kRows>
-__global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs a) {
+// F: the weight format (iq_rows_formats.h); XD: activation dtype (0 f32,
+// 1 f16, 2 bf16); kVecX: activations can be read as aligned 16-byte vectors;
+// kW8A8: fake-quantise x per row first; kRows: 4 or 8, at least m.
+template <class F, int XD, bool kVecX, bool kW8A8, int kRows>
+__global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr uint32_t kT = kRows / 2;  // activation rows per lane: 2t + h
-  constexpr uint32_t kU = rows_units(kRows, kVecX);
+  constexpr uint32_t kU = rows_units<F>(kRows, kVecX);
   uint8_t* xdig = lds + a.xdig_ofs;
   float* xsc = reinterpret_cast<float*>(lds + a.xsc_ofs);
   float* red = reinterpret_cast<float*>(lds + a.xdig_ofs);
@@ -102,7 +114,6 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
   const uint32_t rgl = wave >> (4 - a.rg_shift);
   const uint32_t wp = wave & (P - 1);
   const uint32_t S = 1u << a.slice_shift;
-  const uint32_t row_bytes = a.bpr * kBytesPerBlock;
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, a.x_records);
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.wb, a.wb_records);
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.ws, a.ws_records);
@@ -139,18 +150,23 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
   }
 
   // ---- per-lane constants
-  const uint32_t cg = 16 * (lane & 15);                          // codebook copy
-  const uint32_t cs = RowsTables::kSignBase + 8 * (lane & 15);   // sign-mask copy
-  const uint32_t sel0 = 0x0C0C0000u | ((4u + 2u * h) << 8);      // codebook byte 2h of aux_g
-  const uint32_t sel1 = sel0 + 0x100u;                           // byte 2h + 1
-  const uint32_t rot0 = h ? 7u : 25u, rot1 = h ? 14u : 0u;       // sign fields 2h, 2h + 1
-  uint32_t k27 = 0x07FFFFFFu;
-  asm volatile("" : "+v"(k27));
+  const typename F::Consts fk = F::consts(lane);
   // A row l%32 = (activation row, plane); plane 3 and absent rows read zeros
   const uint32_t ai = lane & 31, axr = ai >> 2, ap = ai & 3;
   const uint32_t aplane = (ap == 3 || axr >= a.m) ? 3u * kRows : axr * 3 + ap;
-  const uint32_t a_base = a.xdig_ofs + aplane * a.plane_stride + 16 * h;
+  const uint32_t a_base = a.xdig_ofs + aplane * a.plane_stride + (F::kHalf ? 8 : 16) * h;
   const uint32_t xs_base = a.xsc_ofs + h * kT * 4;
+  // activation scales of rows 2 tt + h for slice sub-block sub
+  auto load_xs = [&](float* xs, uint32_t sub) {
+    if constexpr (kT == 4) {
+      const u32x4 v = lds_u4(xs_base + sub * kRows * 4);
+      xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
+      xs[2] = __uint_as_float(v.z); xs[3] = __uint_as_float(v.w);
+    } else {
+      const u32x2 v = lds_u2(xs_base + sub * kRows * 4);
+      xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
+    }
+  };
 
   // ---- digitisation of one K slice: task = row * (32 S) + 8-column group
   XTask<XD, kVecX> xo[kRowsMaxTasks];
@@ -200,7 +216,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
       }
       if (ok) {
         const int e = digit_exponent(__uint_as_float(mb));
-        const float scale = ldexpf(1.0f, kDigitShift - e);
+        const float scale = ldexpf(1.0f, F::kDigitShift - e);
         uint32_t dg[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) dg[k] = digitize_biased(xv[k], scale);
@@ -215,28 +231,22 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
             make_uint2(p2[0] ^ 0x80808080u, p2[1] ^ 0x80808080u);
         if ((col8 & 3) == 0)
           xsc[(col8 >> 2) * kRows + (xrow & 1) * kT + (xrow >> 1)] =
-              ldexpf(1.0f, e - kDigitShift - 3);
+              ldexpf(1.0f, e - F::kDigitShift - 3);
       }
     }
   };
 
   // ---- weight units: this wave's t-th unit of slice s is half-super-block
   // ul = wp + P * t of the slice (super-block s * S + ul / 2, half ul % 2);
-  // lane (n, h) loads pair 2 (ul % 2) + h of row n
-  u32x4 q[kU];
-  uint32_t draw[kU];
+  // lane (n, h) loads its half of row n's bytes of the unit
+  typename F::Unit q[kU];
   uint32_t row0 = 0;
   auto issue_unit = [&](uint32_t s, uint32_t t) {
     const uint32_t sb0 = s << a.slice_shift;
     const uint32_t ul = wp + P * t;
     const uint32_t row = row0 + n;
     const bool ok = s < a.nslices && ul < 2 * min(S, a.bpr - sb0) && row < a.out_dim;
-    const uint32_t sb = sb0 + (ul >> 1);
-    const uint32_t off =
-        ok ? row * row_bytes + sb * kBytesPerBlock + (ul & 1) * 32 + 16 * h : kOutOfRange;
-    q[t] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kStreamLoad);
-    draw[t] = __builtin_amdgcn_raw_buffer_load_b16(
-        rs, ok ? (row * a.bpr + sb) * kScalesPerBlock : kOutOfRange, 0, 0);
+    q[t] = F::load(rw, rs, ok, row * a.bpr + sb0 + (ul >> 1), ul & 1, h);
   };
 
   float acc[kT];
@@ -244,7 +254,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
   for (uint32_t chunk = blockIdx.x; chunk < a.nchunks; chunk += gridDim.x) {
     if (chunk != blockIdx.x) sync();  // the previous chunk's flags are read
     row0 = (chunk * R + rgl) * 32;
-    const uint32_t code = (!tables_ready && tid < 256) ? kGridCodesDev[tid] : 0u;
+    const uint32_t code = !tables_ready ? F::seed(tid) : 0u;
     if (tid == 0) *s_special = 0;
     // set-up loads ahead of the weights: the first slice's activations, then a
     // barrier (which does not wait for loads), so that every wave's activation
@@ -254,13 +264,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
 #pragma unroll
     for (uint32_t t = 0; t < kRowsUnitsEarly && t < kU; ++t) issue_unit(0, t);
     if (!tables_ready) {
-      if (tid < 256) {
-        store_grid_row<true>(lds, tid, code);
-      } else if (tid < 512) {
-        const uint32_t i = (tid - 256) >> 1, half = tid & 1;
-        store_sign_row<true>(lds, i, sign_mask(i), half * (RowsTables::kSignCopies / 2),
-                             RowsTables::kSignCopies / 2);
-      }
+      F::tables(lds, tid, code);
       tables_ready = true;
     }
 #pragma unroll
@@ -285,57 +289,45 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
         if (s == 0 && t + kRowsUnitsEarly < kU) issue_unit(0, t + kRowsUnitsEarly);
         const uint32_t ul = wp + P * t;
         if (ul >= 2 * s_eff) break;  // uniform
-        // words of the unit's 4 sub-blocks for this lane's row: lane (n, 0)
-        // holds the unit's first pair, lane (n, 1) its second; v_permlane32_swap
-        // of a register with itself gives every lane both halves' values
-        uint32_t gw[4], sw[4];
-#pragma unroll
-        for (uint32_t c = 0; c < 4; ++c) {
-          const auto r = __builtin_amdgcn_permlane32_swap(q[t][c], q[t][c], false, false);
-          const uint32_t j0 = c >> 1, j1 = j0 + 2;
-          if (c & 1) {
-            sw[j0] = r[0];
-            sw[j1] = r[1];
-          } else {
-            gw[j0] = r[0];
-            gw[j1] = r[1];
-          }
-        }
-        const float dq = half_bits_to_float((uint16_t)draw[t]) * 0x1p-27f;
+        // the codes of the unit's 4 sub-blocks for this lane's row
+        const typename F::Words w = F::unpack(q[t]);
+        const float dq = F::unit_scale(q[t]);
         issue_unit(s + 1, t);  // the registers are free: prefetch
         float au[kT];
 #pragma unroll
         for (uint32_t tt = 0; tt < kT; ++tt) au[tt] = 0.0f;
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j) {
-          const uint32_t sub = ul * 4 + j;  // sub-block in the slice
-          const uint32_t ga0 = __builtin_amdgcn_perm(gw[j], cg, sel0);
-          const uint32_t ga1 = __builtin_amdgcn_perm(gw[j], cg, sel1);
-          const uint32_t sa0 = (__builtin_amdgcn_alignbit(sw[j], sw[j], rot0) & 0x3F80u) | cs;
-          const uint32_t sa1 = (__builtin_amdgcn_alignbit(sw[j], sw[j], rot1) & 0x3F80u) | cs;
-          const u32x4 g0 = lds_u4(ga0), g1 = lds_u4(ga1);
-          const u32x2 m0 = lds_u2(sa0), m1 = lds_u2(sa1);
-          const u32x4 av = lds_u4(a_base + sub * 32);
-          const v4i bw = {(int)bit_select(m0.x, g0.z, g0.x), (int)bit_select(m0.y, g0.w, g0.y),
-                          (int)bit_select(m1.x, g1.z, g1.x), (int)bit_select(m1.y, g1.w, g1.y)};
-          const v4i aw = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
-          const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bw, v16i{}, 0, 0, 0);
-          // (2s+1) * 2^27 (see the one-row kernel), times the activation scales
-          const float sj = (float)((sw[j] & 0xF0000000u) | k27);
-          float xs[kT];
-          if constexpr (kT == 4) {
-            const u32x4 v = lds_u4(xs_base + sub * kRows * 4);
-            xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
-            xs[2] = __uint_as_float(v.z); xs[3] = __uint_as_float(v.w);
-          } else {
-            const u32x2 v = lds_u2(xs_base + sub * kRows * 4);
-            xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
-          }
+        // au += (integer plane sums of c) * scale * xs, activation row 2 tt + h
+        auto accumulate = [&](const v16i& c, float scale, const float* xs) {
 #pragma unroll
           for (uint32_t tt = 0; tt < kT; ++tt) {
             const uint32_t hi = ((uint32_t)c[4 * tt + 2] << 8) + (uint32_t)c[4 * tt + 1];
             const float f = (float)(int)((hi << 8) + (uint32_t)c[4 * tt]);
-            au[tt] = fmaf(f, sj * xs[tt], au[tt]);
+            au[tt] = fmaf(f, scale * xs[tt], au[tt]);
+          }
+        };
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+          const uint32_t sub = ul * 4 + j;  // sub-block in the slice
+          if constexpr (!F::kHalf) {
+            const v4i bw = F::pair(w, j, fk);
+            const u32x4 av = lds_u4(a_base + sub * 32);
+            const v4i aw = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bw, v16i{}, 0, 0, 0);
+            float xs[kT];
+            load_xs(xs, sub);
+            accumulate(c, F::pair_scale(w, j, fk), xs);
+          } else {
+            float xs[kT];
+            load_xs(xs, sub);
+#pragma unroll
+            for (uint32_t hf = 0; hf < 2; ++hf) {
+              const u32x2 bw = F::group(w, j, hf, fk);
+              const u32x2 av = lds_u2(a_base + sub * 32 + 16 * hf);
+              const v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+                  (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bw.y << 32) | bw.x),
+                  v16i{}, 0, 0, 0);
+              accumulate(c, F::group_scale(w, j, hf), xs);
+            }
           }
         }
 #pragma unroll
@@ -387,7 +379,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq2xxs_gemv_rows_kernel(RowsArgs
           if ((__float_as_uint(v) & kAbsMask) < kInfBits) continue;
           for (uint32_t rl = 0; rl < rows; ++rl)
             atomicOr(&s_kinds[rl],
-                     special_kind(v * iq2xxs_weight_at(a.wb, a.ws, chunk_row0 + rl, c, a.bpr)));
+                     special_kind(v * F::weight_at(a.wb, a.ws, chunk_row0 + rl, c, a.bpr)));
         }
         sync();
         for (uint32_t rl = tid; rl < rows; rl += kRowsThreads) {
@@ -422,14 +414,16 @@ struct RowsPlan {
 
 static uint32_t align16r(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
 
-// Launch shape for m (2..8) x out_dim x in_dim on num_cus CUs; false when the
-// shape does not fit (31-bit buffer offsets).
+// Launch shape for m (1..8) x out_dim x in_dim on num_cus CUs for format F;
+// false when the shape does not fit (31-bit buffer offsets, LDS).
+template <class F>
 static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, bool vec,
                       int num_cus, RowsPlan* p) {
   if (m < 1 || m > 8 || out_dim == 0 || in_dim == 0) return false;
   const uint64_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t esize = x_dtype == 0 ? 4 : 2;
-  if ((uint64_t)out_dim * bpr * kBytesPerBlock > kOutOfRange - 4096) return false;
+  if ((uint64_t)out_dim * bpr * F::kBlockBytes > kOutOfRange - 4096) return false;
+  if ((uint64_t)out_dim * bpr * F::kScaleBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)m * in_dim * esize > kOutOfRange - 4096) return false;
   p->rows = m <= 4 ? 4 : 8;
   const uint64_t n_rg = (out_dim + 31) / 32;
@@ -441,70 +435,75 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   p->nchunks = (uint32_t)((n_rg + (1u << rs) - 1) >> rs);
   p->grid = p->nchunks < cus ? p->nchunks : (uint32_t)cus;
   // slice: a power of two of super-blocks, at most kU units per wave and two
-  // digitisation tasks per thread
-  const uint64_t units = rows_units((int)p->rows, vec);
+  // digitisation tasks per thread, whose digits fit in LDS beside the tables
+  const uint64_t units = rows_units<F>((int)p->rows, vec);
   uint32_t ss = 0;
   while (2 * (2ull << ss) <= units * waves_per_rg &&
          (uint64_t)p->rows * (2ull << ss) * 32 <= kRowsMaxTasks * kRowsThreads &&
          (1ull << ss) < bpr)
     ++ss;
-  p->slice_shift = ss;
-  const uint64_t S = 1ull << ss;
-  p->nslices = (uint32_t)((bpr + S - 1) / S);
-  p->plane_stride = (uint32_t)(S * kQK + 16);
-  const uint64_t digits = (3ull * p->rows + 1) * p->plane_stride;
-  const uint64_t partials = (uint64_t)kRowsWaves * (p->rows / 2) * 64 * 4;
-  const uint64_t kinds = (1ull << rs) * 32 * 4;
-  uint64_t region = digits > partials ? digits : partials;
-  region = region > kinds ? region : kinds;
-  p->xdig_ofs = RowsTables::kBytes;
-  p->xsc_ofs = p->xdig_ofs + align16r(region);
-  p->flag_ofs = p->xsc_ofs + align16r(S * 8 * p->rows * 4);
-  p->lds = p->flag_ofs + kRowsFlagBytes;
-  return p->lds <= kGemvLdsLimit;
+  for (;; --ss) {
+    const uint64_t S = 1ull << ss;
+    p->slice_shift = ss;
+    p->nslices = (uint32_t)((bpr + S - 1) / S);
+    p->plane_stride = (uint32_t)(S * kQK + 16);
+    const uint64_t digits = (3ull * p->rows + 1) * p->plane_stride;
+    const uint64_t partials = (uint64_t)kRowsWaves * (p->rows / 2) * 64 * 4;
+    const uint64_t kinds = (1ull << rs) * 32 * 4;
+    uint64_t region = digits > partials ? digits : partials;
+    region = region > kinds ? region : kinds;
+    p->xdig_ofs = F::kTableBytes;
+    p->xsc_ofs = p->xdig_ofs + align16r(region);
+    p->flag_ofs = p->xsc_ofs + align16r(S * 8 * p->rows * 4);
+    p->lds = p->flag_ofs + kRowsFlagBytes;
+    if (p->lds <= kGemvLdsLimit) return true;
+    if (ss == 0) return false;
+  }
 }
 
 bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
   RowsPlan p;
-  return plan_rows(m, out_dim, in_dim, x_dtype, false, 1, &p);
+  return plan_rows<RowsFmtXXS>(m, out_dim, in_dim, x_dtype, false, 1, &p);
 }
 
-template <int XD, bool V, bool Q, int ROWS>
+template <class F, int XD, bool V, bool Q, int ROWS>
 static hipError_t launch_rows_t(const RowsArgs& a, const RowsPlan& p, hipStream_t stream) {
   // The tables alone exceed the default 64 KB of dynamic LDS: raise the
   // limit once per instantiation.
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&iq2xxs_gemv_rows_kernel<XD, V, Q, ROWS>),
+        reinterpret_cast<const void*>(&iq_gemv_rows_kernel<F, XD, V, Q, ROWS>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsLimit);
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
-  hipLaunchKernelGGL((iq2xxs_gemv_rows_kernel<XD, V, Q, ROWS>), dim3(p.grid),
-                     dim3(kRowsThreads), p.lds, stream, a);
+  hipLaunchKernelGGL((iq_gemv_rows_kernel<F, XD, V, Q, ROWS>), dim3(p.grid), dim3(kRowsThreads),
+                     p.lds, stream, a);
   return hipGetLastError();
 }
 
-template <int XD, bool V>
+template <class F, int XD, bool V>
 static hipError_t launch_rows_v(const RowsArgs& a, const RowsPlan& p, bool w8a8,
                                 hipStream_t stream) {
   if (w8a8)
-    return p.rows == 4 ? launch_rows_t<XD, V, true, 4>(a, p, stream)
-                       : launch_rows_t<XD, V, true, 8>(a, p, stream);
-  return p.rows == 4 ? launch_rows_t<XD, V, false, 4>(a, p, stream)
-                     : launch_rows_t<XD, V, false, 8>(a, p, stream);
+    return p.rows == 4 ? launch_rows_t<F, XD, V, true, 4>(a, p, stream)
+                       : launch_rows_t<F, XD, V, true, 8>(a, p, stream);
+  return p.rows == 4 ? launch_rows_t<F, XD, V, false, 4>(a, p, stream)
+                     : launch_rows_t<F, XD, V, false, 8>(a, p, stream);
 }
 
-hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
-                                   const uint8_t* ws, float* out, uint32_t out_dim,
-                                   uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
-                                   const float* gate) {
+// One launch for m <= 8 rows.
+template <class F>
+static hipError_t launch_rows_fmt(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                                  const uint8_t* ws, float* out, uint32_t out_dim,
+                                  uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
+                                  const float* gate) {
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                    ((size_t)in_dim * esize % 16 == 0);
   RowsPlan p;
-  if (!plan_rows(m, out_dim, in_dim, x_dtype, vec, num_cus, &p)) return hipErrorInvalidValue;
+  if (!plan_rows<F>(m, out_dim, in_dim, x_dtype, vec, num_cus, &p)) return hipErrorInvalidValue;
   RowsArgs a;
   a.x = x;
   a.wb = wb;
@@ -519,8 +518,8 @@ hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const
   a.nchunks = p.nchunks;
   a.slice_shift = p.slice_shift;
   a.nslices = p.nslices;
-  a.wb_records = out_dim * a.bpr * kBytesPerBlock;
-  a.ws_records = out_dim * a.bpr * kScalesPerBlock;
+  a.wb_records = out_dim * a.bpr * F::kBlockBytes;
+  a.ws_records = out_dim * a.bpr * F::kScaleBytes;
   a.x_records = m * in_dim * (x_dtype == 0 ? 4u : 2u);
   a.plane_stride = p.plane_stride;
   a.xdig_ofs = p.xdig_ofs;
@@ -528,13 +527,69 @@ hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const
   a.flag_ofs = p.flag_ofs;
   a.gate = gate;
   switch (x_dtype) {
-    case 0: return vec ? launch_rows_v<0, true>(a, p, w8a8, stream)
-                       : launch_rows_v<0, false>(a, p, w8a8, stream);
-    case 1: return vec ? launch_rows_v<1, true>(a, p, w8a8, stream)
-                       : launch_rows_v<1, false>(a, p, w8a8, stream);
-    default: return vec ? launch_rows_v<2, true>(a, p, w8a8, stream)
-                        : launch_rows_v<2, false>(a, p, w8a8, stream);
+    case 0: return vec ? launch_rows_v<F, 0, true>(a, p, w8a8, stream)
+                       : launch_rows_v<F, 0, false>(a, p, w8a8, stream);
+    case 1: return vec ? launch_rows_v<F, 1, true>(a, p, w8a8, stream)
+                       : launch_rows_v<F, 1, false>(a, p, w8a8, stream);
+    default: return vec ? launch_rows_v<F, 2, true>(a, p, w8a8, stream)
+                        : launch_rows_v<F, 2, false>(a, p, w8a8, stream);
   }
+}
+
+hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                                   const uint8_t* ws, float* out, uint32_t out_dim,
+                                   uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
+                                   const float* gate) {
+  return launch_rows_fmt<RowsFmtXXS>(x, x_dtype, m, wb, ws, out, out_dim, in_dim, w8a8, num_cus,
+                                     stream, gate);
+}
+
+template <class F>
+static bool variant_rows_fit(uint32_t out_dim, uint32_t in_dim, int x_dtype) {
+  RowsPlan p;
+  return plan_rows<F>(8, out_dim, in_dim, x_dtype, false, 1, &p) &&
+         plan_rows<F>(4, out_dim, in_dim, x_dtype, true, 1, &p);
+}
+
+bool variant_rows_supported(int variant, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
+  switch (variant) {
+    case 1: return variant_rows_fit<RowsFmtXS>(out_dim, in_dim, x_dtype);
+    case 2: return variant_rows_fit<RowsFmtS>(out_dim, in_dim, x_dtype);
+    case 3: return variant_rows_fit<RowsFmtS3>(out_dim, in_dim, x_dtype);
+    default: return false;
+  }
+}
+
+hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint32_t m,
+                                  const uint8_t* wb, const uint8_t* ws, float* out,
+                                  uint32_t out_dim, uint32_t in_dim, bool w8a8, int num_cus,
+                                  hipStream_t stream) {
+  const size_t esize = x_dtype == 0 ? 4 : 2;
+  // groups of 8 activation rows, each a launch that reads every weight once
+  for (uint32_t r0 = 0; r0 < m; r0 += 8) {
+    const uint32_t mr = m - r0 < 8 ? m - r0 : 8;
+    const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize;
+    float* o = out + (size_t)r0 * out_dim;
+    hipError_t e;
+    switch (variant) {
+      case 1:
+        e = launch_rows_fmt<RowsFmtXS>(xr, x_dtype, mr, wb, ws, o, out_dim, in_dim, w8a8,
+                                       num_cus, stream, nullptr);
+        break;
+      case 2:
+        e = launch_rows_fmt<RowsFmtS>(xr, x_dtype, mr, wb, ws, o, out_dim, in_dim, w8a8,
+                                      num_cus, stream, nullptr);
+        break;
+      case 3:
+        e = launch_rows_fmt<RowsFmtS3>(xr, x_dtype, mr, wb, ws, o, out_dim, in_dim, w8a8,
+                                       num_cus, stream, nullptr);
+        break;
+      default:
+        return hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace cmk

@@ -83,6 +83,14 @@ hipError_t launch_iq_variant_matmul(int variant, const void* x, int x_dtype, uin
                                     const uint8_t* wb, const uint8_t* ws, float* out,
                                     uint32_t out_dim, uint32_t in_dim, const float* row_inv,
                                     int num_cus, hipStream_t stream);
+// The multi-row decode kernel for IQ2_XS (1), IQ2_S (2), IQ3_S (3): any m, in
+// launches of up to 8 rows; W8A8 row scales computed in the kernel.  Needs
+// weight_bytes 16-byte and weight_scales 2-byte aligned.
+bool variant_rows_supported(int variant, uint32_t out_dim, uint32_t in_dim, int x_dtype);
+hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint32_t m,
+                                  const uint8_t* wb, const uint8_t* ws, float* out,
+                                  uint32_t out_dim, uint32_t in_dim, bool w8a8, int num_cus,
+                                  hipStream_t stream);
 hipError_t launch_iq_variant_dequant(int variant, const uint8_t* wb, const uint8_t* ws, void* out,
                                      int out_kind, uint32_t out_dim, uint32_t in_dim, int num_cus,
                                      hipStream_t stream);

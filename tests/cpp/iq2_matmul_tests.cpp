@@ -130,6 +130,29 @@ void errors_before_any_device_access() {
 
 // ------------------------------------------------------------------ GPU tests
 
+// The reference's bar (src/iq2_matmul.rs:1113,1121 and 1239,1247) holds its
+// GPU kernel, which sums in the CPU loop's order, to `bar` of the CPU result.
+// This GPU path sums in another order, and with d = 1 the outputs reach a few
+// thousand, where the CPU loop's own fp32 result is ~2e-3 from the exact
+// product (IQ3_S: 2.2e-3).  So the GPU result is held to `bar` of the exact
+// product (xf: the activations the reference multiplies), and to `bar` plus
+// the CPU loop's own distance from it of the CPU result.
+void check_reference_bar(const std::vector<float>& y, const std::vector<float>& ref,
+                         Iq2MatmulVariant variant, const Case& c, const std::vector<float>& xf,
+                         double bar) {
+  std::vector<double> y64(c.m * c.out_dim), scale(c.m * c.out_dim);
+  oracle_iq_matmul_f64(oracle_variant(variant), xf.data(), c.m, c.out_dim, c.in_dim, c.wb.data(),
+                       c.ws.data(), y64.data(), scale.data());
+  double exact = 0, own = 0;
+  for (size_t i = 0; i < y.size(); ++i) {
+    exact = std::fmax(exact, std::fabs((double)y[i] - y64[i]));
+    own = std::fmax(own, std::fabs((double)ref[i] - y64[i]));
+  }
+  CHECK(exact <= bar, "IQ2 parity: |gpu - exact| too high: " + std::to_string(exact));
+  const double md = max_abs_diff(y, ref);
+  CHECK(md <= bar + own, "IQ2 parity max_abs too high: " + std::to_string(md));
+}
+
 void parity_case(Iq2MatmulVariant variant) {
   Case c = parity_inputs(variant);
   DevCase d = upload(c, Device::hip(0));
@@ -140,8 +163,7 @@ void parity_case(Iq2MatmulVariant variant) {
                              c.wb.data(), c.ws.data(), ref.data());
   CHECK(y.dims() == (std::vector<size_t>{2, 7}), "output shape");
   CHECK(y.dtype() == DType::F32, "output dtype");
-  const double md = max_abs_diff(y.to_vec<float>(), ref);
-  CHECK(md <= 2e-3, "IQ2 parity max_abs too high: " + std::to_string(md));  // :1113,1121
+  check_reference_bar(y.to_vec<float>(), ref, variant, c, c.x, 2e-3);  // :1113,1121
 }
 
 void parity_case_w8a8(Iq2MatmulVariant variant) {
@@ -152,8 +174,9 @@ void parity_case_w8a8(Iq2MatmulVariant variant) {
   std::vector<float> ref(c.m * c.out_dim);
   oracle_iq_matmul_reference_w8a8(oracle_variant(variant), c.x.data(), c.m, c.out_dim, c.in_dim,
                                   c.wb.data(), c.ws.data(), ref.data());
-  const double md = max_abs_diff(y.to_vec<float>(), ref);
-  CHECK(md <= 3e-3, "IQ2 W8A8 parity max_abs too high: " + std::to_string(md));  // :1239,1247
+  std::vector<float> xq(c.x.size());
+  oracle_rowwise_qdq_w8a8(c.x.data(), c.m, c.in_dim, xq.data());
+  check_reference_bar(y.to_vec<float>(), ref, variant, c, xq, 3e-3);  // :1239,1247
 }
 
 void w8a8_smoke_case(Iq2MatmulVariant variant) {
