@@ -49,6 +49,8 @@ size_t scales_per_block(int v) { return v == CMK_IQ2_XXS ? 2 : cmk::variant_scal
 // rows.  f16 / bf16 x switch at 8 rows, where the two are level in time.
 constexpr size_t kGemvMaxM = 8;
 constexpr size_t kGemvMaxMF32 = 16;
+// W8A8 activations are int8 on the multi-row kernel, 32 rows per launch.
+constexpr size_t kGemvMaxMW8A8 = 32;
 constexpr size_t kWorkspaceAlign = 256;
 
 bool checked_mul(size_t a, size_t b, size_t* out) {
@@ -87,12 +89,13 @@ enum class Path { Gemv, Gemm, Simple, Variant };
 // Null pointers stand for allocator-aligned buffers (queries made before the
 // buffers exist).
 Path choose_path(int x_dtype, size_t m, uint32_t out_dim, uint32_t in_dim, const void* x,
-                 const void* wb, const void* ws) {
+                 const void* wb, const void* ws, bool w8a8) {
   auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; };
   // f32 rows beyond the GEMV's range are staged as scaled f16 head / tail row
   // pairs for the GEMM (twice the rows).
   const size_t gemm_rows = x_dtype == CMK_F32 ? 2 * m : m;
-  const size_t gemv_max_m = x_dtype == CMK_F32 ? kGemvMaxMF32 : kGemvMaxM;
+  const size_t gemv_max_m =
+      w8a8 ? kGemvMaxMW8A8 : (x_dtype == CMK_F32 ? kGemvMaxMF32 : kGemvMaxM);
   if (m > gemv_max_m && gemm_rows <= UINT32_MAX &&
       cmk::gemm_supported((uint32_t)gemm_rows, out_dim, in_dim) && al(x, 16) && al(wb, 16) &&
       al(ws, 2))
@@ -241,7 +244,8 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
   // Assume allocator-aligned buffers (hipMalloc gives 256-byte alignment).
   Path p = variant != CMK_IQ2_XXS
                ? Path::Variant
-               : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, nullptr, nullptr, nullptr);
+               : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, nullptr, nullptr, nullptr,
+                             md == CMK_ACT_QUANT_W8A8);
   // The simple path can still be chosen at launch for unaligned weights; report
   // the larger need so either choice is covered.
   size_t need =
@@ -254,10 +258,9 @@ int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, s
 
 int cmk_iq2_matmul_path(cmk_dtype x_dtype, size_t m, size_t out_dim, size_t in_dim,
                         cmk_act_quant_mode mode) {
-  (void)mode;
   return choose_path((int)x_dtype, m, (uint32_t)(out_dim > UINT32_MAX ? UINT32_MAX : out_dim),
                      (uint32_t)(in_dim > UINT32_MAX ? UINT32_MAX : in_dim), nullptr, nullptr,
-                     nullptr) == Path::Gemm
+                     nullptr, mode == CMK_ACT_QUANT_W8A8) == Path::Gemm
              ? 1
              : 0;
 }
@@ -290,7 +293,7 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   const bool w8a8 = md == CMK_ACT_QUANT_W8A8;
   Path p = variant != CMK_IQ2_XXS ? Path::Variant
                                   : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x,
-                                                weight_bytes, weight_scales);
+                                                weight_bytes, weight_scales, w8a8);
   const size_t need_ws = workspace_for(p, w8a8, (int)x_dtype, m, dims.out_dim, dims.in_dim);
   const size_t head_ws = workspace_head(p, w8a8, (int)x_dtype, m, dims.in_dim);
   if (need_ws > 0 && (workspace == nullptr || workspace_bytes < need_ws))
@@ -363,7 +366,8 @@ int cmk_iq2_matmul_noalloc(const void* x, cmk_dtype x_dtype, size_t x_len, size_
   if (m == 0) return ok();
   const Path p = variant != CMK_IQ2_XXS ? Path::Variant
                                         : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim,
-                                                      x, weight_bytes, weight_scales);
+                                                      x, weight_bytes, weight_scales,
+                                                      md == CMK_ACT_QUANT_W8A8);
   const size_t need =
       workspace_for(p, md == CMK_ACT_QUANT_W8A8, (int)x_dtype, m, dims.out_dim, dims.in_dim);
   if (need > (size_t)CMK_IQ2_NOALLOC_SCRATCH_BYTES)
@@ -517,8 +521,8 @@ int cmk_iq2_matmul_swiglu(const void* x, cmk_dtype x_dtype, size_t x_len, size_t
   const uintptr_t g0 = reinterpret_cast<uintptr_t>(gate), o0 = reinterpret_cast<uintptr_t>(out);
   if (g0 < o0 + need_out * 4 && o0 < g0 + need_out * 4)
     return fail(CMK_ERR_INVALID_ARGUMENT, "matmul_swiglu gate must not overlap out");
-  if (choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x, weight_bytes, weight_scales) !=
-      Path::Gemv)
+  if (choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x, weight_bytes, weight_scales,
+                  false) != Path::Gemv)
     return fail(CMK_ERR_UNSUPPORTED,
                 "matmul_swiglu serves the decode-shaped kernels (m <= %zu for F32 x, <= %zu for "
                 "F16/BF16, aligned weights): use cmk_iq2_matmul and cmk_swiglu",

@@ -208,12 +208,19 @@ __device__ __forceinline__ float special_value(uint32_t kinds) {
   return 0.0f;
 }
 
-// W8A8 fake quantisation of one activation (src/metal_src/iq2_matmul.metal:98-102):
-// q = clamp(round_half_away(x * inv), -127, 127); return q / inv.
-__device__ __forceinline__ float qdq_w8a8(float x, float inv_scale) {
+// W8A8 quantisation of one activation (src/iq2_matmul.rs:1025-1048,
+// iq2_matmul.metal:98-102): q = clamp(round_half_away(x * inv), -127, 127), an
+// integer in a float.  A NaN stays NaN, as in the reference's CPU path
+// (f32::clamp); the Metal clamp (fmin/fmax) would give -127 instead.
+__device__ __forceinline__ float quant_w8a8(float x, float inv_scale) {
   float q = roundf(x * inv_scale);
-  q = fminf(fmaxf(q, -127.0f), 127.0f);
-  return q / inv_scale;
+  q = q < -127.0f ? -127.0f : q;
+  return q > 127.0f ? 127.0f : q;
+}
+
+// The reference's fake quantisation: q / inv.
+__device__ __forceinline__ float qdq_w8a8(float x, float inv_scale) {
+  return quant_w8a8(x, inv_scale) / inv_scale;
 }
 
 // ---------------------------------------------------------------------------

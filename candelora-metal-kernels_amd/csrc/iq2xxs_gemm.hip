@@ -530,8 +530,8 @@ __global__ __launch_bounds__(256) void iq2xxs_quantize_rows_kernel(const uint16_
       const float lo = kBf16 ? bf16_bits_to_float((uint16_t)w[k]) : half_bits_to_float((uint16_t)w[k]);
       const float hi = kBf16 ? bf16_bits_to_float((uint16_t)(w[k] >> 16))
                              : half_bits_to_float((uint16_t)(w[k] >> 16));
-      const float ql = fminf(fmaxf(roundf(lo * inv), -127.0f), 127.0f);
-      const float qh = fminf(fmaxf(roundf(hi * inv), -127.0f), 127.0f);
+      const float ql = quant_w8a8(lo, inv);
+      const float qh = quant_w8a8(hi, inv);
       o[k] = pack2<kBf16>(ql, qh);
     }
     *reinterpret_cast<u32x4*>(q + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
@@ -551,13 +551,11 @@ __global__ __launch_bounds__(256) void iq2xxs_stage_f32_w8a8_kernel(const float*
     const float inv = row_inv[c / chunks_per_row];
     const float4 lo = *reinterpret_cast<const float4*>(x + c * 8);
     const float4 hi = *reinterpret_cast<const float4*>(x + c * 8 + 4);
-    const float v[8] = {lo.x * inv, lo.y * inv, lo.z * inv, lo.w * inv,
-                        hi.x * inv, hi.y * inv, hi.z * inv, hi.w * inv};
+    const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     uint32_t o[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      o[k] = pack2<false>(fminf(fmaxf(roundf(v[2 * k]), -127.0f), 127.0f),
-                          fminf(fmaxf(roundf(v[2 * k + 1]), -127.0f), 127.0f));
+      o[k] = pack2<false>(quant_w8a8(v[2 * k], inv), quant_w8a8(v[2 * k + 1], inv));
     *reinterpret_cast<u32x4*>(q + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
   }
 }

@@ -29,6 +29,9 @@
 //    d*(2s+1)/8 * 2^(e-20) is applied in fp32.
 //  * A wave sums its 16 blocks with DPP and lane-swap moves; the workgroup
 //    adds the slices of a row in slice order.  Results are deterministic.
+//  * W8A8 (true int8): the reference's q = clamp(round(x * inv), +-127) is
+//    digit plane 0 as it stands (planes 1 and 2 are zero), so the sub-block
+//    sums of q times the codes are exact; each output is divided by inv once.
 //
 // Schedule.  A CU's memory pipeline serves requests roughly in issue order and
 // a wave that issues a load stalls while the pipeline is full, so the order of
@@ -325,12 +328,17 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (uint32_t u = 0; u < (uint32_t)kXT; ++u) {
       const uint32_t task = r0 + u * kGemvThreads + rtid;
-      float xv[8];
+      float xv[8], qv[8];
       uint32_t mb = 0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         xv[k] = xo[u].get(k);
-        if constexpr (kW8A8) xv[k] = qdq_w8a8(xv[k], inv_scale);
+        if constexpr (kW8A8) {
+          // xv only flags values whose q / inv is not finite: for inv >=
+          // 2^-100, |q / inv| <= 127 * 2^100 is finite unless q is NaN
+          qv[k] = quant_w8a8(xv[k], inv_scale);
+          xv[k] = inv_scale >= 0x1p-100f ? qv[k] : qv[k] / inv_scale;
+        }
         mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
       }
       mb = quad_max_u32(mb);
@@ -339,13 +347,26 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const uint32_t ab = __float_as_uint(xv[k]) & kAbsMask;
-          if (ab >= kInfBits) xv[k] = 0.0f;
+          if (ab >= kInfBits) {
+            xv[k] = 0.0f;
+            if constexpr (kW8A8) qv[k] = 0.0f;
+          }
           mb = max(mb, ab < kInfBits ? ab : 0u);
         }
         mb = quad_max_u32(mb);
         if (task < a.ntasks) *s_special = gen;
       }
-      if (task < a.ntasks) {
+      if (kW8A8 && task < a.ntasks) {
+        // q as plane 0, planes 1 and 2 zero; the scale keeps the weights' 1/8
+        uint32_t qb[2] = {0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qb[k >> 2] |= ((uint32_t)(int)qv[k] & 0xFFu) << (8 * (k & 3));
+        const uint32_t c0 = (task >> 2) * 32 + (task & 3) * 8;
+        *reinterpret_cast<uint2*>(xdig + c0) = make_uint2(qb[0], qb[1]);
+        *reinterpret_cast<uint2*>(xdig + a.plane_stride + c0) = make_uint2(0u, 0u);
+        *reinterpret_cast<uint2*>(xdig + 2 * a.plane_stride + c0) = make_uint2(0u, 0u);
+        if ((task & 3) == 0) xsc[task >> 2] = 0.125f;
+      } else if (task < a.ntasks) {
         const int e = digit_exponent(__uint_as_float(mb));
         const float scale = ldexpf(1.0f, kDigitShift - e);
         // biased digit bytes (each digit + 128), transposed into planes, then
@@ -544,7 +565,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       float sum = 0.0f;
       for (uint32_t sl = 0; sl < a.nslices; ++sl) sum += p[sl * 4];
       const size_t o = (size_t)mrow * a.out_dim + row_begin + rl;
-      a.out[o] = gated ? silu_mul(a.gate[o], sum) : sum;
+      const float v = kW8A8 ? sum / inv_row : sum;  // W8A8: q / inv
+      a.out[o] = gated ? silu_mul(a.gate[o], v) : v;
     }
     if (special) {
       fix_up_special(mrow);
@@ -701,7 +723,9 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
 }
 
 bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
-  if (m > 1) return gemv_rows_supported(m < 8 ? m : 8, out_dim, in_dim, x_dtype);
+  if (m > 1)
+    return gemv_rows_supported(m < 8 ? m : 8, out_dim, in_dim, x_dtype, false) &&
+           gemv_rows_supported(m < 32 ? m : 32, out_dim, in_dim, x_dtype, true);
   GemvPlan p;
   return plan_gemv(m, out_dim, in_dim, x_dtype, 1, &p);
 }
@@ -752,13 +776,14 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream, const float* gate) {
   if (m > 1) {
-    // groups of up to 8 activation rows, each decoding the weights once
+    // groups of up to 8 activation rows (W8A8: 32), each decoding the weights once
     const size_t esize = x_dtype == 0 ? 4 : 2;
-    for (uint32_t r0 = 0; r0 < m; r0 += 8) {
+    const uint32_t group = w8a8 ? 32 : 8;
+    for (uint32_t r0 = 0; r0 < m; r0 += group) {
       const hipError_t e = launch_iq2xxs_gemv_rows(
           static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize, x_dtype,
-          m - r0 < 8 ? m - r0 : 8, wb, ws, out + (size_t)r0 * out_dim, out_dim, in_dim, w8a8,
-          num_cus, stream, gate ? gate + (size_t)r0 * out_dim : nullptr);
+          m - r0 < group ? m - r0 : group, wb, ws, out + (size_t)r0 * out_dim, out_dim, in_dim,
+          w8a8, num_cus, stream, gate ? gate + (size_t)r0 * out_dim : nullptr);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -1,5 +1,6 @@
-// iq2xxs_gemv_rows.hip — IQ2_XXS matmul for 2..8 activation rows, and IQ2_XS,
-// IQ2_S and IQ3_S matmuls for up to 8 rows per launch, on gfx950.
+// iq2xxs_gemv_rows.hip — IQ2_XXS matmul for 2..8 activation rows (W8A8: up
+// to 32), and IQ2_XS, IQ2_S and IQ3_S matmuls for up to 8 rows per launch
+// (W8A8: 32), on gfx950.
 //
 // Replaces iq2_xxs_matmul_kernel / iq2_xxs_matmul_w8a8_kernel
 // (src/metal_src/iq2_matmul.metal:188-240, 436-499) for small m > 1, and the
@@ -38,6 +39,16 @@
 // unpacked.  The waves of a row group add their partial sums in wave order,
 // so results are deterministic.
 //
+// W8A8 (true int8).  The reference fake-quantises x per row (q / inv with q =
+// clamp(round(x * inv), +-127), iq2_matmul.metal:85-126) and multiplies in
+// fp32.  Here q itself is the A operand: one int8 plane per activation row, so
+// the 32 A rows are 32 activation rows and one launch serves up to 32 rows
+// (kRows 8 keeps the four result registers of rows 0..7, kRows 32 all 16).
+// The sub-block sums of q times the codes are exact in int32; (2s+1) d is
+// applied per sub-block in fp32 and 1 / (8 inv) once per output.  A value
+// whose q / inv is not finite (an infinite x, or every x of a row that holds
+// one, where inv = 0) is set aside and fixed up like a non-finite x.
+//
 // Bound: HBM (the same algorithmic bytes as the one-row kernel; every weight
 // byte is read once, x once per workgroup from L2).
 #include <atomic>
@@ -59,7 +70,8 @@ constexpr uint32_t kRowsMaxTasks = 2;  // digitisation tasks per thread and slic
 // at issue while it is full, so weight requests issued ahead of a barrier
 // would hold every wave at that barrier until they drain.
 constexpr uint32_t kRowsUnitsEarly = 1;
-constexpr uint32_t kRowsFlagBytes = 1024;
+// Flags and the W8A8 row scales.
+constexpr uint32_t rows_flag_bytes(uint32_t rows) { return (16 + 4 * rows + 15) & ~15u; }
 
 struct RowsArgs {
   const void* x;
@@ -80,29 +92,33 @@ struct RowsArgs {
   const float* gate;
 };
 
-// Units a wave holds per slice: four for up to 4 rows read as vectors with
-// IQ2_XXS's 5-register units, two otherwise (the registers a 1024-thread
-// workgroup leaves a wave: 128).
+// Units a wave holds per slice: four with IQ2_XXS's 5-register units, x read
+// as vectors and at most four result registers (up to 4 rows; W8A8 up to 8),
+// two otherwise (the registers a 1024-thread workgroup leaves a wave: 128).
 template <class F>
-constexpr uint32_t rows_units(int rows, bool vec) {
-  return rows == 4 && vec && sizeof(typename F::Unit) <= 20 ? 4 : 2;
+constexpr uint32_t rows_units(int rows, bool vec, bool w8a8) {
+  return rows == (w8a8 ? 8 : 4) && vec && sizeof(typename F::Unit) <= 20 ? 4 : 2;
 }
 
 // F: the weight format (iq_rows_formats.h); XD: activation dtype (0 f32,
 // 1 f16, 2 bf16); kVecX: activations can be read as aligned 16-byte vectors;
-// kW8A8: fake-quantise x per row first; kRows: 4 or 8, at least m.
+// kW8A8: int8 activations q (kRows 8 or 32); otherwise kRows is 4 or 8; at
+// least m.
 template <class F, int XD, bool kVecX, bool kW8A8, int kRows>
 __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr uint32_t kT = kRows / 2;  // activation rows per lane: 2t + h
-  constexpr uint32_t kU = rows_units<F>(kRows, kVecX);
+  // result registers kept per lane: W8A8 the first kRows / 2 (activation rows
+  // 8 (r/4) + 4 h + r % 4), otherwise the plane sums folded into kT rows
+  constexpr uint32_t kAcc = kT;
+  static_assert(!kW8A8 || kRows == 8 || kRows == 32, "W8A8 runs 8 or 32 rows per launch");
+  constexpr uint32_t kU = rows_units<F>(kRows, kVecX, kW8A8);
   uint8_t* xdig = lds + a.xdig_ofs;
   float* xsc = reinterpret_cast<float*>(lds + a.xsc_ofs);
   float* red = reinterpret_cast<float*>(lds + a.xdig_ofs);
   uint32_t* s_kinds = reinterpret_cast<uint32_t*>(lds + a.xdig_ofs);
   uint32_t* s_special = reinterpret_cast<uint32_t*>(lds + a.flag_ofs);  // bit r: row r not finite
-  float* s_inv = reinterpret_cast<float*>(lds + a.flag_ofs + 16);      // W8A8 scales, 8 rows
-  float* s_wred = reinterpret_cast<float*>(lds + a.flag_ofs + 64);     // 16 waves x 8 rows
+  float* s_inv = reinterpret_cast<float*>(lds + a.flag_ofs + 16);      // W8A8 scales
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63;
@@ -123,37 +139,42 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // ---- W8A8 row scales (iq2_matmul.metal:86-96): 127 / max|x_r|
+  // ---- W8A8 row scales (iq2_matmul.metal:86-96): 127 / max|x_r|.  Wave w
+  // takes rows w, w + 16: its lanes read the row as 8-element tasks, eight per
+  // lane in flight (K = 4096 in one round trip), and the wave reduces them (fmaxf drops a NaN, as the
+  // reference's max does).
   if constexpr (kW8A8) {
-    float mx[kRows];
+    constexpr uint32_t kBatch = 8;
+    const uint32_t tpr = (a.in_dim + 7) / 8;  // tasks per row
+    for (uint32_t r = wave; r < a.m; r += kRowsWaves) {
+      float mx = 0.0f;
+      for (uint32_t t0 = 0; t0 < tpr; t0 += 64 * kBatch) {
+        XTask<XD, kVecX> xt[kBatch];
 #pragma unroll
-    for (uint32_t r = 0; r < (uint32_t)kRows; ++r) mx[r] = 0.0f;
-    for (uint32_t c = tid; c < a.in_dim; c += kRowsThreads)
+        for (uint32_t u = 0; u < kBatch; ++u) {
+          const uint32_t t = t0 + u * 64 + lane;
+          xt[u].load(rx, r * a.in_dim + 8 * t, 8 * t, a.in_dim, t < tpr);
+        }
 #pragma unroll
-      for (uint32_t r = 0; r < (uint32_t)kRows; ++r)
-        if (r < a.m)
-          mx[r] = fmaxf(mx[r], fabsf(x_bits_to_float<XD>(
-                                   load_x_bits<XD>(a.x, (size_t)r * a.in_dim + c))));
+        for (uint32_t u = 0; u < kBatch; ++u)
 #pragma unroll
-    for (uint32_t r = 0; r < (uint32_t)kRows; ++r) {
+          for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(xt[u].get(k)));
+      }
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off));
-      if (lane == 0) s_wred[wave * 8 + r] = mx[r];
-    }
-    sync();
-    if (tid < (uint32_t)kRows) {
-      float v = 0.0f;
-      for (uint32_t w = 0; w < kRowsWaves; ++w) v = fmaxf(v, s_wred[w * 8 + tid]);
-      s_inv[tid] = (v < 1e-8f) ? 1.0f : 127.0f / v;
+      for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      if (lane == 0) s_inv[r] = (mx < 1e-8f) ? 1.0f : 127.0f / mx;
     }
     sync();
   }
 
   // ---- per-lane constants
   const typename F::Consts fk = F::consts(lane);
-  // A row l%32 = (activation row, plane); plane 3 and absent rows read zeros
+  // A row l%32 = (activation row, plane); plane 3 and absent rows read zeros.
+  // W8A8: A row l%32 = activation row l%32 (its q); rows from m on read zeros.
   const uint32_t ai = lane & 31, axr = ai >> 2, ap = ai & 3;
-  const uint32_t aplane = (ap == 3 || axr >= a.m) ? 3u * kRows : axr * 3 + ap;
+  const uint32_t zero_plane = kW8A8 ? a.m : 3u * kRows;
+  const uint32_t aplane = kW8A8 ? (ai < a.m ? ai : zero_plane)
+                                : ((ap == 3 || axr >= a.m) ? zero_plane : axr * 3 + ap);
   const uint32_t a_base = a.xdig_ofs + aplane * a.plane_stride + (F::kHalf ? 8 : 16) * h;
   const uint32_t xs_base = a.xsc_ofs + h * kT * 4;
   // activation scales of rows 2 tt + h for slice sub-block sub
@@ -193,13 +214,18 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
       const uint32_t col8 = task & (32 * S - 1);
       const bool ok = xrow < a.m && col8 < 32 * s_eff;  // same on the 4 lanes of a quad
       float inv = 1.0f;
-      if constexpr (kW8A8) inv = s_inv[min(xrow, 7u)];
-      float xv[8];
+      if constexpr (kW8A8) inv = s_inv[min(xrow, kRows - 1u)];
+      float xv[8], qv[8];
       uint32_t mb = 0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         xv[k] = xo[u].get(k);
-        if constexpr (kW8A8) xv[k] = qdq_w8a8(xv[k], inv);
+        if constexpr (kW8A8) {
+          // xv only flags values whose q / inv is not finite: for inv >=
+          // 2^-100, |q / inv| <= 127 * 2^100 is finite unless q is NaN
+          qv[k] = quant_w8a8(xv[k], inv);
+          xv[k] = inv >= 0x1p-100f ? qv[k] : qv[k] / inv;
+        }
         mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
       }
       mb = quad_max_u32(mb);
@@ -208,13 +234,26 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const uint32_t ab = __float_as_uint(xv[k]) & kAbsMask;
-          if (ab >= kInfBits) xv[k] = 0.0f;
+          if (ab >= kInfBits) {
+            xv[k] = 0.0f;
+            if constexpr (kW8A8) qv[k] = 0.0f;
+          }
           mb = max(mb, ab < kInfBits ? ab : 0u);
         }
         mb = quad_max_u32(mb);
         if (ok) atomicOr(s_special, 1u << xrow);
       }
-      if (ok) {
+      if constexpr (kW8A8) {
+        // the row's plane: q as signed bytes
+        if (ok) {
+          uint32_t qb[2] = {0, 0};
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            qb[k >> 2] |= ((uint32_t)(int)qv[k] & 0xFFu) << (8 * (k & 3));
+          *reinterpret_cast<uint2*>(xdig + xrow * a.plane_stride + col8 * 8) =
+              make_uint2(qb[0], qb[1]);
+        }
+      } else if (ok) {
         const int e = digit_exponent(__uint_as_float(mb));
         const float scale = ldexpf(1.0f, F::kDigitShift - e);
         uint32_t dg[8];
@@ -249,7 +288,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     q[t] = F::load(rw, rs, ok, row * a.bpr + sb0 + (ul >> 1), ul & 1, h);
   };
 
-  float acc[kT];
+  float acc[kAcc];
   bool tables_ready = false;
   for (uint32_t chunk = blockIdx.x; chunk < a.nchunks; chunk += gridDim.x) {
     if (chunk != blockIdx.x) sync();  // the previous chunk's flags are read
@@ -268,7 +307,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
       tables_ready = true;
     }
 #pragma unroll
-    for (uint32_t t = 0; t < kT; ++t) acc[t] = 0.0f;
+    for (uint32_t t = 0; t < kAcc; ++t) acc[t] = 0.0f;
 
     // One K slice: digits of slice s (its activations are in flight), then
     // this wave's units of slice s (each prefetches the next slice's unit).
@@ -277,7 +316,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     auto run_slice = [&](uint32_t s) {
       // the zero plane (its area is rewritten by the partial sums at the end)
       if (tid < 16 * S)
-        *reinterpret_cast<u32x4*>(xdig + 3 * kRows * a.plane_stride + 16 * tid) =
+        *reinterpret_cast<u32x4*>(xdig + zero_plane * a.plane_stride + 16 * tid) =
             u32x4{0, 0, 0, 0};
       digitize(s);
       sync();
@@ -296,13 +335,22 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
         float au[kT];
 #pragma unroll
         for (uint32_t tt = 0; tt < kT; ++tt) au[tt] = 0.0f;
-        // au += (integer plane sums of c) * scale * xs, activation row 2 tt + h
+        // c: this lane's 16 results of one MFMA; scale: the sub-scale of its
+        // columns.  Digits: au += (integer plane sums of c) * scale * xs,
+        // activation row 2 tt + h.  W8A8: acc += c * (2s+1) d, exact int32
+        // sums of q (|c| < 2^24) times an exact scale.
         auto accumulate = [&](const v16i& c, float scale, const float* xs) {
+          if constexpr (kW8A8) {
+            const float sd = scale * dq;
 #pragma unroll
-          for (uint32_t tt = 0; tt < kT; ++tt) {
-            const uint32_t hi = ((uint32_t)c[4 * tt + 2] << 8) + (uint32_t)c[4 * tt + 1];
-            const float f = (float)(int)((hi << 8) + (uint32_t)c[4 * tt]);
-            au[tt] = fmaf(f, scale * xs[tt], au[tt]);
+            for (uint32_t r = 0; r < kAcc; ++r) acc[r] = fmaf((float)c[r], sd, acc[r]);
+          } else {
+#pragma unroll
+            for (uint32_t tt = 0; tt < kT; ++tt) {
+              const uint32_t hi = ((uint32_t)c[4 * tt + 2] << 8) + (uint32_t)c[4 * tt + 1];
+              const float f = (float)(int)((hi << 8) + (uint32_t)c[4 * tt]);
+              au[tt] = fmaf(f, scale * xs[tt], au[tt]);
+            }
           }
         };
 #pragma unroll
@@ -314,11 +362,11 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
             const v4i aw = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
             const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bw, v16i{}, 0, 0, 0);
             float xs[kT];
-            load_xs(xs, sub);
+            if constexpr (!kW8A8) load_xs(xs, sub);
             accumulate(c, F::pair_scale(w, j, fk), xs);
           } else {
             float xs[kT];
-            load_xs(xs, sub);
+            if constexpr (!kW8A8) load_xs(xs, sub);
 #pragma unroll
             for (uint32_t hf = 0; hf < 2; ++hf) {
               const u32x2 bw = F::group(w, j, hf, fk);
@@ -330,8 +378,10 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
             }
           }
         }
+        if constexpr (!kW8A8) {
 #pragma unroll
-        for (uint32_t tt = 0; tt < kT; ++tt) acc[tt] = fmaf(au[tt], dq, acc[tt]);
+          for (uint32_t tt = 0; tt < kT; ++tt) acc[tt] = fmaf(au[tt], dq, acc[tt]);
+        }
       }
     };
     sync();  // tables and the cleared flag
@@ -343,21 +393,50 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     }
 
     // ---- the P waves of a row group add their partial sums in wave order
-    sync();
-#pragma unroll
-    for (uint32_t tt = 0; tt < kT; ++tt) red[((rgl * P + wp) * kT + tt) * 64 + lane] = acc[tt];
-    sync();
     const uint32_t chunk_row0 = chunk * R * 32;
-    const uint32_t special = *s_special;  // uniform (final since the last digitisation)
-    const bool gated = a.gate != nullptr && special == 0;
-    for (uint32_t o = tid; o < R * kT * 64; o += kRowsThreads) {
-      const uint32_t ol = o & 63, tt = (o >> 6) % kT, rg = (o >> 6) / kT;
-      float sum = 0.0f;
-      for (uint32_t w = 0; w < P; ++w) sum += red[((rg * P + w) * kT + tt) * 64 + ol];
-      const uint32_t xrow = 2 * tt + (ol >> 5), row = chunk_row0 + rg * 32 + (ol & 31);
-      if (xrow < a.m && row < a.out_dim) {
-        const size_t i = (size_t)xrow * a.out_dim + row;
-        a.out[i] = gated ? silu_mul(a.gate[i], sum) : sum;
+    uint32_t special = 0;
+    bool gated = false;
+    if constexpr (kW8A8) {
+      // four result registers at a time: activation rows 8 g + 4 h + i
+#pragma unroll
+      for (uint32_t g = 0; g < kAcc / 4; ++g) {
+        if (8 * g >= a.m) break;  // uniform
+        sync();
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i)
+          red[((rgl * P + wp) * 4 + i) * 64 + lane] = acc[4 * g + i];
+        sync();
+        special = *s_special;  // uniform (final since the last digitisation)
+        gated = a.gate != nullptr && special == 0;
+        for (uint32_t o = tid; o < R * 4 * 64; o += kRowsThreads) {
+          const uint32_t ol = o & 63, i = (o >> 6) & 3, rg = o >> 8;
+          float sum = 0.0f;
+          for (uint32_t w = 0; w < P; ++w) sum += red[((rg * P + w) * 4 + i) * 64 + ol];
+          const uint32_t xrow = 8 * g + 4 * (ol >> 5) + i, row = chunk_row0 + rg * 32 + (ol & 31);
+          if (xrow < a.m && row < a.out_dim) {
+            const size_t oi = (size_t)xrow * a.out_dim + row;
+            const float v = sum * 0.125f / s_inv[xrow];  // q / inv, and the weights' 1/8
+            a.out[oi] = gated ? silu_mul(a.gate[oi], v) : v;
+          }
+        }
+      }
+    } else {
+      sync();
+#pragma unroll
+      for (uint32_t tt = 0; tt < kT; ++tt)
+        red[((rgl * P + wp) * kT + tt) * 64 + lane] = acc[tt];
+      sync();
+      special = *s_special;  // uniform (final since the last digitisation)
+      gated = a.gate != nullptr && special == 0;
+      for (uint32_t o = tid; o < R * kT * 64; o += kRowsThreads) {
+        const uint32_t ol = o & 63, tt = (o >> 6) % kT, rg = (o >> 6) / kT;
+        float sum = 0.0f;
+        for (uint32_t w = 0; w < P; ++w) sum += red[((rg * P + w) * kT + tt) * 64 + ol];
+        const uint32_t xrow = 2 * tt + (ol >> 5), row = chunk_row0 + rg * 32 + (ol & 31);
+        if (xrow < a.m && row < a.out_dim) {
+          const size_t i = (size_t)xrow * a.out_dim + row;
+          a.out[i] = gated ? silu_mul(a.gate[i], sum) : sum;
+        }
       }
     }
 
@@ -414,18 +493,20 @@ struct RowsPlan {
 
 static uint32_t align16r(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
 
-// Launch shape for m (1..8) x out_dim x in_dim on num_cus CUs for format F;
-// false when the shape does not fit (31-bit buffer offsets, LDS).
+// Launch shape for m (1..8; W8A8 1..32) x out_dim x in_dim on num_cus CUs for
+// format F; false when the shape does not fit (31-bit buffer offsets, LDS).
 template <class F>
 static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, bool vec,
-                      int num_cus, RowsPlan* p) {
-  if (m < 1 || m > 8 || out_dim == 0 || in_dim == 0) return false;
+                      bool w8a8, int num_cus, RowsPlan* p) {
+  if (m < 1 || m > (w8a8 ? 32u : 8u) || out_dim == 0 || in_dim == 0) return false;
   const uint64_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t esize = x_dtype == 0 ? 4 : 2;
   if ((uint64_t)out_dim * bpr * F::kBlockBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)out_dim * bpr * F::kScaleBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)m * in_dim * esize > kOutOfRange - 4096) return false;
-  p->rows = m <= 4 ? 4 : 8;
+  p->rows = w8a8 ? (m <= 8 ? 8 : 32) : (m <= 4 ? 4 : 8);
+  // activation rows digitised per slice (W8A8 digitises the m rows only)
+  const uint64_t task_rows = w8a8 ? m : p->rows;
   const uint64_t n_rg = (out_dim + 31) / 32;
   const uint64_t cus = num_cus > 0 ? (uint64_t)num_cus : 1;
   uint32_t rs = 0;
@@ -436,10 +517,10 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   p->grid = p->nchunks < cus ? p->nchunks : (uint32_t)cus;
   // slice: a power of two of super-blocks, at most kU units per wave and two
   // digitisation tasks per thread, whose digits fit in LDS beside the tables
-  const uint64_t units = rows_units<F>((int)p->rows, vec);
+  const uint64_t units = rows_units<F>((int)p->rows, vec, w8a8);
   uint32_t ss = 0;
   while (2 * (2ull << ss) <= units * waves_per_rg &&
-         (uint64_t)p->rows * (2ull << ss) * 32 <= kRowsMaxTasks * kRowsThreads &&
+         task_rows * (2ull << ss) * 32 <= kRowsMaxTasks * kRowsThreads &&
          (1ull << ss) < bpr)
     ++ss;
   for (;; --ss) {
@@ -447,23 +528,25 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
     p->slice_shift = ss;
     p->nslices = (uint32_t)((bpr + S - 1) / S);
     p->plane_stride = (uint32_t)(S * kQK + 16);
-    const uint64_t digits = (3ull * p->rows + 1) * p->plane_stride;
-    const uint64_t partials = (uint64_t)kRowsWaves * (p->rows / 2) * 64 * 4;
+    // digit planes and the zero plane; W8A8: the rows' q and the zero plane
+    const uint64_t digits = (w8a8 ? m + 1ull : 3ull * p->rows + 1) * p->plane_stride;
+    const uint64_t partials = (uint64_t)kRowsWaves * (w8a8 ? 4 : p->rows / 2) * 64 * 4;
     const uint64_t kinds = (1ull << rs) * 32 * 4;
     uint64_t region = digits > partials ? digits : partials;
     region = region > kinds ? region : kinds;
     p->xdig_ofs = F::kTableBytes;
     p->xsc_ofs = p->xdig_ofs + align16r(region);
-    p->flag_ofs = p->xsc_ofs + align16r(S * 8 * p->rows * 4);
-    p->lds = p->flag_ofs + kRowsFlagBytes;
+    p->flag_ofs = p->xsc_ofs + (w8a8 ? 0u : align16r(S * 8 * p->rows * 4));
+    p->lds = p->flag_ofs + rows_flag_bytes(p->rows);
     if (p->lds <= kGemvLdsLimit) return true;
     if (ss == 0) return false;
   }
 }
 
-bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
+bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype,
+                         bool w8a8) {
   RowsPlan p;
-  return plan_rows<RowsFmtXXS>(m, out_dim, in_dim, x_dtype, false, 1, &p);
+  return plan_rows<RowsFmtXXS>(m, out_dim, in_dim, x_dtype, false, w8a8, 1, &p);
 }
 
 template <class F, int XD, bool V, bool Q, int ROWS>
@@ -487,13 +570,13 @@ template <class F, int XD, bool V>
 static hipError_t launch_rows_v(const RowsArgs& a, const RowsPlan& p, bool w8a8,
                                 hipStream_t stream) {
   if (w8a8)
-    return p.rows == 4 ? launch_rows_t<F, XD, V, true, 4>(a, p, stream)
-                       : launch_rows_t<F, XD, V, true, 8>(a, p, stream);
+    return p.rows == 8 ? launch_rows_t<F, XD, V, true, 8>(a, p, stream)
+                       : launch_rows_t<F, XD, V, true, 32>(a, p, stream);
   return p.rows == 4 ? launch_rows_t<F, XD, V, false, 4>(a, p, stream)
                      : launch_rows_t<F, XD, V, false, 8>(a, p, stream);
 }
 
-// One launch for m <= 8 rows.
+// One launch for m <= 8 rows (W8A8: m <= 32).
 template <class F>
 static hipError_t launch_rows_fmt(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                   const uint8_t* ws, float* out, uint32_t out_dim,
@@ -503,7 +586,8 @@ static hipError_t launch_rows_fmt(const void* x, int x_dtype, uint32_t m, const 
   const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                    ((size_t)in_dim * esize % 16 == 0);
   RowsPlan p;
-  if (!plan_rows<F>(m, out_dim, in_dim, x_dtype, vec, num_cus, &p)) return hipErrorInvalidValue;
+  if (!plan_rows<F>(m, out_dim, in_dim, x_dtype, vec, w8a8, num_cus, &p))
+    return hipErrorInvalidValue;
   RowsArgs a;
   a.x = x;
   a.wb = wb;
@@ -547,8 +631,9 @@ hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const
 template <class F>
 static bool variant_rows_fit(uint32_t out_dim, uint32_t in_dim, int x_dtype) {
   RowsPlan p;
-  return plan_rows<F>(8, out_dim, in_dim, x_dtype, false, 1, &p) &&
-         plan_rows<F>(4, out_dim, in_dim, x_dtype, true, 1, &p);
+  return plan_rows<F>(8, out_dim, in_dim, x_dtype, false, false, 1, &p) &&
+         plan_rows<F>(4, out_dim, in_dim, x_dtype, true, false, 1, &p) &&
+         plan_rows<F>(32, out_dim, in_dim, x_dtype, false, true, 1, &p);
 }
 
 bool variant_rows_supported(int variant, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
@@ -565,9 +650,11 @@ hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint3
                                   uint32_t out_dim, uint32_t in_dim, bool w8a8, int num_cus,
                                   hipStream_t stream) {
   const size_t esize = x_dtype == 0 ? 4 : 2;
-  // groups of 8 activation rows, each a launch that reads every weight once
-  for (uint32_t r0 = 0; r0 < m; r0 += 8) {
-    const uint32_t mr = m - r0 < 8 ? m - r0 : 8;
+  // groups of 8 activation rows (W8A8: 32), each a launch that reads every
+  // weight once
+  const uint32_t group = w8a8 ? 32 : 8;
+  for (uint32_t r0 = 0; r0 < m; r0 += group) {
+    const uint32_t mr = m - r0 < group ? m - r0 : group;
     const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize;
     float* o = out + (size_t)r0 * out_dim;
     hipError_t e;

@@ -26,8 +26,9 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream,
                               const float* gate = nullptr);
-// The multi-row kernel alone (1 <= m <= 8).
-bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype);
+// The multi-row kernel alone (1 <= m <= 8; W8A8: 1 <= m <= 32).
+bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype,
+                         bool w8a8 = false);
 hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                    const uint8_t* ws, float* out, uint32_t out_dim,
                                    uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
@@ -84,7 +85,8 @@ hipError_t launch_iq_variant_matmul(int variant, const void* x, int x_dtype, uin
                                     uint32_t out_dim, uint32_t in_dim, const float* row_inv,
                                     int num_cus, hipStream_t stream);
 // The multi-row decode kernel for IQ2_XS (1), IQ2_S (2), IQ3_S (3): any m, in
-// launches of up to 8 rows; W8A8 row scales computed in the kernel.  Needs
+// launches of up to 8 rows (W8A8: 32, int8 activations; row scales computed in
+// the kernel).  Needs
 // weight_bytes 16-byte and weight_scales 2-byte aligned.
 bool variant_rows_supported(int variant, uint32_t out_dim, uint32_t in_dim, int x_dtype);
 hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint32_t m,

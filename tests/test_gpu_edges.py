@@ -82,6 +82,36 @@ def test_gemv_nonfinite_x(pkg, oracle, inputs, dev, pattern, dtype, m, out_dim, 
         assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
 
 
+@pytest.mark.parametrize("m", [1, 3, 40])
+def test_w8a8_nonfinite_x(pkg, oracle, inputs, dev, m):
+    """W8A8 with an infinite activation (row 0: inv = 0, so every q / inv of
+    the row is NaN or infinite) and a NaN (row 1: NaN through the clamp, as in
+    the reference's CPU path): output classes exactly as the oracle's, the
+    finite rows to the GEMV bar (m = 1: the one-row kernel, 3: the int8
+    multi-row kernel, 40: the GEMM)."""
+    out_dim, in_dim = 1024, 4096
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    x = inputs.synthetic_x(m, in_dim)
+    x[0, 5] = np.inf
+    if m > 1:
+        x[1, 77] = np.nan
+    dtype = torch.float16 if m == 40 else torch.float32
+    xt = x_tensor(x, dtype, dev)
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    y = pkg.iq2_matmul_with_activation_quant(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim,
+                                             in_dim, pkg.Iq2MatmulVariant.Iq2Xxs, cfg)
+    y = y.cpu().numpy()
+    xf = x_as_f32(xt)
+    ref = oracle.matmul_reference_w8a8(xf, m, out_dim, in_dim, wb, ws)
+    assert np.array_equal(classes(y), classes(ref))
+    assert np.all(np.isnan(y[0])) and (m == 1 or np.all(np.isnan(y[1])))
+    if m == 3:  # (the GEMM's numerics have their own tests)
+        xq = oracle.rowwise_qdq_w8a8(xf[2:], 1, in_dim)
+        y64, sc = oracle.matmul_f64(xq, 1, out_dim, in_dim, wb, ws)
+        cond, rel = errors(y[2:], y64, sc)
+        assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+
+
 @pytest.mark.parametrize("pattern", ["nan", "posinf", "both_inf"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_gemm_nonfinite_x(pkg, oracle, inputs, dev, pattern, dtype):

@@ -104,8 +104,9 @@ def test_variant_rows_unaligned_x_element_loads(pkg, oracle, dev, v, dtype):
 
 
 @pytest.mark.parametrize("v", VARIANTS)
-@pytest.mark.parametrize("m", [1, 4, 7])
+@pytest.mark.parametrize("m", [1, 4, 7, 20, 32, 40])
 def test_variant_rows_w8a8(pkg, oracle, dev, v, m):
+    """W8A8: int8 q, up to 32 rows per launch (40: 32 + 8)."""
     out_dim, in_dim = 777, 3000
     wb, ws = random_weights(oracle, v, out_dim, in_dim, 90 + v + m)
     xt = to_dev(_x(m, in_dim, 95 + v + m), dev).to(torch.float16)
