@@ -101,10 +101,10 @@ class Matmul:
     pointers, so the tensors must stay alive as long as the launch (or a graph
     that captured it) can run."""
 
-    def __init__(self, cabi, x, wb, ws, out, m, k, n, x_dtype, stream, variant=0):
+    def __init__(self, cabi, x, wb, ws, out, m, k, n, x_dtype, stream, variant=0, mode=0):
         # the workspace the path asks for (f32 rows staged for the GEMM), allocated once here
         import torch
-        ws_bytes = cabi.workspace_size(x_dtype, m, n, k, variant)
+        ws_bytes = cabi.workspace_size(x_dtype, m, n, k, variant, mode)
         self.workspace = (torch.empty((ws_bytes,), dtype=torch.uint8, device=x.device)
                           if ws_bytes else None)
         self.tensors = (x, wb, ws, out)
@@ -114,10 +114,12 @@ class Matmul:
         self.cabi = cabi
         self.stream = stream
         self.variant = variant
+        self.mode = mode
 
     def __call__(self):
-        self.cabi.matmul_raw(*self.args, variant=self.variant, workspace_ptr=self.ws_args[0],
-                             workspace_bytes=self.ws_args[1], stream=self.stream)
+        self.cabi.matmul_raw(*self.args, variant=self.variant, mode=self.mode,
+                             workspace_ptr=self.ws_args[0], workspace_bytes=self.ws_args[1],
+                             stream=self.stream)
 
 
 def bench_decode(pkg, torch, stream, steps, warmup):
@@ -322,14 +324,15 @@ def _timed_graph(torch, cabi, stream, sh, run, steps):
 
 
 def bench_configs(pkg, torch, stream):
-    """BASELINE config 2 (M in {4, 8, 16}, f32 x, %HBM) and config 4 (the
+    """BASELINE config 2 (M in {4, 8, 16}, f32 x, %HBM; and W8A8 with int8
+    activations, M in {4, 8, 16, 32} at N = 14336) and config 4 (the
     Llama-3-70B layer's seven projections back to back with f32 x: M=1 on the
     GEMV; M=128 rows staged as scaled f16 for the MFMA GEMM, then also with f16
     x given), over rotated weight copies."""
     cabi, inputs = pkg.cabi, pkg.inputs
     dev = torch.device("cuda:0")
     sh = int(stream.cuda_stream)
-    res = {"config2": [], "config4": {}}
+    res = {"config2": [], "config2_w8a8": [], "config4": {}}
     for k, n in ((4096, 4096), (4096, 14336)):
         wb, ws = inputs.synthetic_weights(n, k)
         w_bytes = wb.size + ws.size
@@ -347,6 +350,20 @@ def bench_configs(pkg, torch, stream):
             res["config2"].append({"m": m, "k": k, "n": n, "us": us, "gbs": gbs,
                                    "frac_of_hbm_peak": gbs / HBM_PEAK_GBS})
             log(f"[bench] config 2 m={m} k={k} n={n}: {us:.2f} us, {gbs:.1f} GB/s")
+        for m in ((4, 8, 16, 32) if n == 14336 else ()):
+            x = torch.from_numpy(inputs.synthetic_x(m, k)).to(dev)
+            out = torch.empty((m, n), dtype=torch.float32, device=dev)
+            calls = [Matmul(cabi, x, r[0], r[1], out, m, k, n, cabi.CMK_F32, sh,
+                            mode=cabi.CMK_ACT_QUANT_W8A8) for r in reps]
+            for c in calls:
+                c()
+            us = _timed_graph(torch, cabi, stream, sh, lambda i: calls[i % copies](), 100)
+            gbs = alg_bytes(m, k, n) / (us * 1e-6) / 1e9
+            path = cabi.matmul_path(cabi.CMK_F32, m, n, k, cabi.CMK_ACT_QUANT_W8A8)
+            res["config2_w8a8"].append({"m": m, "k": k, "n": n, "us": us, "gbs": gbs,
+                                        "path": path, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS})
+            log(f"[bench] config 2 W8A8 m={m} k={k} n={n} ({path}): {us:.2f} us, "
+                f"{gbs:.1f} GB/s")
         del reps
     layer_w = sum(nn * math.ceil(kk / 256) * 66 for _, kk, nn in CONFIG4_SHAPES)
     copies = max(2, math.ceil(2 * MALL_BYTES / layer_w))
@@ -690,6 +707,7 @@ def main():
         line["mlp_step_m1"] = mlp
     if configs is not None:
         line["config2_small_m"] = configs["config2"]
+        line["config2_w8a8_int8"] = configs["config2_w8a8"]
         line["config4_70b_layer"] = configs["config4"]
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(pkg, args.cpu_seconds)

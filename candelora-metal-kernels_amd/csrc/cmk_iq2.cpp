@@ -49,7 +49,9 @@ size_t scales_per_block(int v) { return v == CMK_IQ2_XXS ? 2 : cmk::variant_scal
 // rows.  f16 / bf16 x switch at 8 rows, where the two are level in time.
 constexpr size_t kGemvMaxM = 8;
 constexpr size_t kGemvMaxMF32 = 16;
-// W8A8 activations are int8 on the multi-row kernel, 32 rows per launch.
+// W8A8 activations are int8 on the multi-row kernel, 32 rows per launch: at
+// 24 to 32 rows it is level in time with the GEMM (which rounds the weights
+// to f16) and its sums are exact.
 constexpr size_t kGemvMaxMW8A8 = 32;
 constexpr size_t kWorkspaceAlign = 256;
 

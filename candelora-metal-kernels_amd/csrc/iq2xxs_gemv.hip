@@ -333,14 +333,18 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         xv[k] = xo[u].get(k);
-        if constexpr (kW8A8) {
-          // xv only flags values whose q / inv is not finite: for inv >=
-          // 2^-100, |q / inv| <= 127 * 2^100 is finite unless q is NaN
-          qv[k] = quant_w8a8(xv[k], inv_scale);
-          xv[k] = inv_scale >= 0x1p-100f ? qv[k] : qv[k] / inv_scale;
-        }
-        mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
+        if constexpr (kW8A8) xv[k] = qv[k] = quant_w8a8(xv[k], inv_scale);
       }
+      if constexpr (kW8A8) {
+        // xv only flags values whose q / inv is not finite: for inv >= 2^-100,
+        // |q / inv| <= 127 * 2^100 is finite unless q is NaN
+        if (inv_scale < 0x1p-100f) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) xv[k] = qv[k] / inv_scale;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
       mb = quad_max_u32(mb);
       if (mb >= kInfBits) {
         mb = 0;

@@ -220,14 +220,18 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         xv[k] = xo[u].get(k);
-        if constexpr (kW8A8) {
-          // xv only flags values whose q / inv is not finite: for inv >=
-          // 2^-100, |q / inv| <= 127 * 2^100 is finite unless q is NaN
-          qv[k] = quant_w8a8(xv[k], inv);
-          xv[k] = inv >= 0x1p-100f ? qv[k] : qv[k] / inv;
-        }
-        mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
+        if constexpr (kW8A8) xv[k] = qv[k] = quant_w8a8(xv[k], inv);
       }
+      if constexpr (kW8A8) {
+        // xv only flags values whose q / inv is not finite: for inv >= 2^-100,
+        // |q / inv| <= 127 * 2^100 is finite unless q is NaN
+        if (inv < 0x1p-100f) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) xv[k] = qv[k] / inv;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
       mb = quad_max_u32(mb);
       if (mb >= kInfBits) {  // a NaN or an infinity: set aside (fixed up at the end)
         mb = 0;
@@ -331,7 +335,8 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
         // the codes of the unit's 4 sub-blocks for this lane's row
         const typename F::Words w = F::unpack(q[t]);
         const float dq = F::unit_scale(q[t]);
-        issue_unit(s + 1, t);  // the registers are free: prefetch
+        // the registers are free: prefetch (none after the last slice)
+        if (s + 1 < a.nslices) issue_unit(s + 1, t);
         float au[kT];
 #pragma unroll
         for (uint32_t tt = 0; tt < kT; ++tt) au[tt] = 0.0f;

@@ -99,13 +99,15 @@ def test_rows_w8a8(pkg, oracle, inputs, dev, dtype, m):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
-@pytest.mark.parametrize("m", [12, 20, 32])
-def test_rows_w8a8_int8_up_to_32_rows(pkg, oracle, inputs, dev, dtype, m):
+@pytest.mark.parametrize("m", [6, 12, 20, 32])
+def test_rows_w8a8_int8_rows(pkg, oracle, inputs, dev, dtype, m):
     """W8A8 feeds q itself as one int8 plane per activation row, so one launch
-    of the multi-row kernel serves up to 32 rows."""
+    of the multi-row kernel serves up to 32 rows (33 on: the GEMM)."""
     out_dim, in_dim = 1000, 3000
     cd = pkg.cabi.CMK_F32 if dtype == torch.float32 else pkg.cabi.CMK_F16
-    assert pkg.cabi.matmul_path(cd, m, out_dim, in_dim, pkg.cabi.CMK_ACT_QUANT_W8A8) == "gemv"
+    w8 = pkg.cabi.CMK_ACT_QUANT_W8A8
+    assert pkg.cabi.matmul_path(cd, m, out_dim, in_dim, w8) == "gemv"
+    assert pkg.cabi.matmul_path(cd, 33, out_dim, in_dim, w8) == "gemm"
     wb, ws = inputs.synthetic_weights(out_dim, in_dim, seed=m)
     xt = x_tensor(inputs.synthetic_x(m, in_dim, seed=200 + m), dtype, dev)
     _check(pkg, oracle, xt, wb, ws, out_dim, in_dim, dev, w8a8=True)
