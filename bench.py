@@ -607,7 +607,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (for rocprof counter calibration)")
-    ap.add_argument("--only", choices=["decode", "prefill", "read-floor"],
+    ap.add_argument("--only", choices=["decode", "prefill", "read-floor", "variants", "configs"],
                     help="time one line only and print it (for profiling runs)")
     args = ap.parse_args()
 
@@ -645,6 +645,10 @@ def main():
                 res = bench_decode(pkg, torch, stream, args.steps, args.warmup)
             elif args.only == "prefill":
                 res = bench_prefill(pkg, torch, stream, args.prefill_steps, 5)
+            elif args.only == "variants":
+                res = bench_variants(pkg, torch, stream, args.variant_steps)
+            elif args.only == "configs":
+                res = bench_configs(pkg, torch, stream)
             else:
                 res = bench_read_floor(pkg, torch, stream, args.steps * len(DECODE_SHAPES))
         torch.cuda.synchronize()
