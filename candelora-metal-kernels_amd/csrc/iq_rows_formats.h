@@ -43,6 +43,12 @@
 
 namespace cmk {
 
+// Cache policy of the unit loads: default.  A unit reads 32 bytes of each of
+// 32 rows, so the four units of a 128-byte line come from four waves; with
+// the nontemporal hint a line could leave the cache between them (M=4, N=14336:
+// 12.5 us with the hint, 11.5 us without).
+constexpr int kUnitLoad = 0;
+
 static __constant__ uint16_t kRowsXsCodes[512] = {CMK_IQ2XS_GRID_CODES};
 static __constant__ uint16_t kRowsSCodes[1024] = {CMK_IQ2S_GRID_CODES};
 static __constant__ uint16_t kRowsS3Codes[512] = {CMK_IQ3S_GRID_CODES};
@@ -126,7 +132,7 @@ struct RowsFmtXXS {
                               uint32_t blk, uint32_t half, uint32_t h) {
     Unit u;
     const uint32_t off = ok ? blk * kBlockBytes + half * 32 + 16 * h : kOutOfRange;
-    u.q = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kStreamLoad);
+    u.q = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kUnitLoad);
     u.d = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? blk * kScaleBytes : kOutOfRange, 0, 0);
     return u;
   }
@@ -213,7 +219,7 @@ struct RowsFmtXS {
                               uint32_t blk, uint32_t half, uint32_t h) {
     Unit u;
     const uint32_t off = ok ? blk * kBlockBytes + half * 32 + 16 * h : kOutOfRange;
-    u.q = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kStreamLoad);
+    u.q = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kUnitLoad);
     const uint32_t so = ok ? blk * kScaleBytes : kOutOfRange;
     u.d = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
     u.s01 = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so + 2 + 4 * half : kOutOfRange, 0, 0);
@@ -308,11 +314,11 @@ struct RowsFmtS {
     Unit u;
     const uint32_t base = blk * kBlockBytes;
     u.qs = __builtin_amdgcn_raw_buffer_load_b64(
-        rw, ok ? base + 16 * half + 8 * h : kOutOfRange, 0, kStreamLoad);
+        rw, ok ? base + 16 * half + 8 * h : kOutOfRange, 0, kUnitLoad);
     u.sg = __builtin_amdgcn_raw_buffer_load_b64(
-        rw, ok ? base + 32 + 16 * half + 8 * h : kOutOfRange, 0, kStreamLoad);
+        rw, ok ? base + 32 + 16 * half + 8 * h : kOutOfRange, 0, kUnitLoad);
     u.qh = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? base + 64 + 4 * half : kOutOfRange,
-                                                0, kStreamLoad);
+                                                0, kUnitLoad);
     const uint32_t so = ok ? blk * kScaleBytes : kOutOfRange;
     u.d = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
     u.s01 = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so + 2 + 4 * half : kOutOfRange, 0, 0);
@@ -412,14 +418,14 @@ struct RowsFmtS3 {
     const uint32_t base = blk * kBlockBytes;
     // (blocks are 8-byte aligned only: the 16 code bytes as two 8-byte loads)
     const uint32_t qo = ok ? base + 32 * half + 16 * h : kOutOfRange;
-    const u32x2 q0 = __builtin_amdgcn_raw_buffer_load_b64(rw, qo, 0, kStreamLoad);
+    const u32x2 q0 = __builtin_amdgcn_raw_buffer_load_b64(rw, qo, 0, kUnitLoad);
     const u32x2 q1 = __builtin_amdgcn_raw_buffer_load_b64(rw, ok ? qo + 8 : kOutOfRange, 0,
-                                                          kStreamLoad);
+                                                          kUnitLoad);
     u.qs = u32x4{q0.x, q0.y, q1.x, q1.y};
     u.sg = __builtin_amdgcn_raw_buffer_load_b64(
-        rw, ok ? base + 72 + 16 * half + 8 * h : kOutOfRange, 0, kStreamLoad);
+        rw, ok ? base + 72 + 16 * half + 8 * h : kOutOfRange, 0, kUnitLoad);
     u.qh = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? base + 64 + 4 * half : kOutOfRange,
-                                                0, kStreamLoad);
+                                                0, kUnitLoad);
     const uint32_t so = ok ? blk * kScaleBytes : kOutOfRange;
     u.d = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
     u.sc = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so + 2 + 2 * half : kOutOfRange, 0, 0);
