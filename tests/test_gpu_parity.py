@@ -10,7 +10,10 @@ Bars:
       rel   = max over outputs with |y64_i| >= 1e-2 max|y64| of |y_i - y64_i|/|y64_i|
               (<= 1e-3, the GEMV bar)
   * MFMA GEMM (x f16/bf16, large m): against x @ dequant_{f16,bf16}(W)^T in fp64
-    with cond <= 1e-4 and rel <= 1e-2 (the GEMM bar).
+    with cond <= 1e-4 and rel <= 1e-2 (the GEMM bar); and against the reference's
+    path on the same inputs (the fp64 oracle with exact weights) within the
+    weights' unit roundoff, cond <= u + 1e-5 (f16: u = 2^-11, bf16: 2^-8), since
+    each weight is one RNE of its exact value.
 """
 
 import numpy as np
@@ -47,6 +50,26 @@ def errors(y, y64, scale):
     cond = float(np.max(np.abs(y - y64) / np.maximum(scale, 1e-300)))
     big = np.abs(y64) >= 1e-2 * np.max(np.abs(y64))
     rel = float(np.max(np.abs(y - y64)[big] / np.abs(y64[big]))) if big.any() else 0.0
+    return cond, rel
+
+
+# Unit roundoff of the GEMM's weights: each is one RNE of its exact value
+# (f16: 11 significant bits, bf16: 8), so against the exact product
+# |y - y_exact| <= u * sum_k |x_k w_k| plus the fp32 accumulation.
+W_ROUNDOFF = {"f16": 2.0 ** -11, "bf16": 2.0 ** -8}
+
+
+def check_vs_reference_path(oracle, y, x_f32, wb, ws, out_dim, in_dim, wfmt):
+    """The GEMM against the reference's path on the same inputs: the fp64
+    oracle product with exact weights (x_f32: the activations the reference
+    multiplies, W8A8 already quantised)."""
+    m = x_f32.shape[0]
+    if m * out_dim * in_dim > 6e8:
+        return None  # (the single-threaded fp64 oracle would take tens of seconds)
+    y64, sc = oracle.matmul_f64(np.ascontiguousarray(x_f32, np.float32), m, out_dim, in_dim, wb,
+                                ws)
+    cond, rel = errors(y, y64, sc)
+    assert cond <= W_ROUNDOFF[wfmt] + 1e-5, (wfmt, cond, rel)
     return cond, rel
 
 
@@ -248,6 +271,8 @@ def test_gemm_vs_dequant_matmul(pkg, oracle, inputs, dev, dtype, m, out_dim, in_
     sc = np.abs(x64) @ np.abs(w).T
     cond, rel = errors(y, y64, sc)
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+    check_vs_reference_path(oracle, y, x_as_f32(xt), wb, ws, out_dim, in_dim,
+                            "f16" if dtype == torch.float16 else "bf16")
 
 
 def test_gemm_w8a8(pkg, oracle, inputs, dev):
@@ -263,6 +288,7 @@ def test_gemm_w8a8(pkg, oracle, inputs, dev):
     y64 = xq @ w.T
     cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+    check_vs_reference_path(oracle, y, xq.astype(np.float32), wb, ws, out_dim, in_dim, "f16")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -304,6 +330,7 @@ def test_gemm_w8a8_bf16_ragged(pkg, oracle, inputs, dev):
     wbits = oracle.dequantize_bf16_bits(wb, ws, out_dim, in_dim).astype(np.uint32) << 16
     w = wbits.view(np.float32).astype(np.float64)
     y64 = xq @ w.T
+    check_vs_reference_path(oracle, y, xq.astype(np.float32), wb, ws, out_dim, in_dim, "bf16")
     cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
 
@@ -340,6 +367,7 @@ def test_gemm_f32_rows_staged(pkg, oracle, inputs, dev, m, out_dim, in_dim):
     for rows in (slice(0, 1), slice(1, 2), slice(3, m)):  # each row band against its own scale
         cond, rel = errors(y[rows], y64[rows], np.abs(x64[rows]) @ np.abs(w).T)
         assert cond <= 1e-5 and rel <= 1e-3, (rows, cond, rel)
+        check_vs_reference_path(oracle, y[rows], x[rows], wb, ws, out_dim, in_dim, "f16")
 
 
 def test_gemm_f32_rows_w8a8(pkg, oracle, inputs, dev):
@@ -355,6 +383,7 @@ def test_gemm_f32_rows_w8a8(pkg, oracle, inputs, dev):
     y64 = xq @ w.T
     cond, rel = errors(y, y64, np.abs(xq) @ np.abs(w).T)
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+    check_vs_reference_path(oracle, y, xq.astype(np.float32), wb, ws, out_dim, in_dim, "f16")
 
 
 def test_gemm_k_split_deterministic(pkg, oracle, inputs, dev):
