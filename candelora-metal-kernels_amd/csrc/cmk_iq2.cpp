@@ -114,12 +114,12 @@ size_t row_scale_bytes(size_t m) {
 }
 
 // Row scales and staged rows at the head of the workspace: the GEMM stages
-// f32 rows (as head / tail pairs) and W8A8 rows; Simple and Variant need the
-// W8A8 row scales only.
+// f32 rows (as head / tail pairs), bf16 rows (as scaled f16) and W8A8 rows;
+// Simple and Variant need the W8A8 row scales only.
 size_t workspace_head(Path p, bool w8a8, int x_dtype, size_t m, uint32_t in_dim) {
   if (p == Path::Gemm && x_dtype == CMK_F32)
     return row_scale_bytes(m) + cmk::gemm_f32_scratch_bytes((uint32_t)m, in_dim, w8a8);
-  if (p == Path::Gemm && w8a8)
+  if (p == Path::Gemm && (w8a8 || x_dtype == CMK_BF16))  // (bf16 rows staged as f16)
     return row_scale_bytes(m) + cmk::gemm_w8a8_scratch_bytes((uint32_t)m, in_dim);
   if (!w8a8 || p == Path::Gemv) return 0;
   return row_scale_bytes(m);

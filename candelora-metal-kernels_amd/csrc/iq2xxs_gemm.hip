@@ -509,8 +509,8 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   }
 }
 
-// W8A8 pre-pass: q = clamp(round_half_away(x * inv_row), -127, 127) in the
-// activation's type (exact), eight activations per thread.
+// W8A8 pre-pass: q = clamp(round_half_away(x * inv_row), -127, 127) from f16
+// or bf16 activations, written as f16 (exact), eight activations per thread.
 template <bool kBf16>
 __global__ __launch_bounds__(256) void iq2xxs_quantize_rows_kernel(const uint16_t* x, uint32_t m,
                                                                    uint32_t in_dim,
@@ -532,9 +532,55 @@ __global__ __launch_bounds__(256) void iq2xxs_quantize_rows_kernel(const uint16_
                              : half_bits_to_float((uint16_t)(w[k] >> 16));
       const float ql = quant_w8a8(lo, inv);
       const float qh = quant_w8a8(hi, inv);
-      o[k] = pack2<kBf16>(ql, qh);
+      o[k] = pack2<false>(ql, qh);
     }
     *reinterpret_cast<u32x4*>(q + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// bf16 rows for the f16 GEMM (f16 weights carry 11 significant bits, bf16
+// weights 8): one workgroup per row scales the row by the power of two inv
+// that brings its largest finite magnitude into [2^14, 2^15) and writes
+// x * inv as f16, exact for every value at or above 2^-31 of the row's
+// largest (bf16 has 8 significant bits); inv goes to row_inv, which the
+// epilogue divides by.  NaN and infinities stay what they are.
+__global__ __launch_bounds__(256) void iq2xxs_scale_stage_bf16_rows_kernel(
+    const uint16_t* __restrict__ x, uint32_t in_dim, float* __restrict__ row_inv,
+    uint16_t* __restrict__ q) {
+  __shared__ uint32_t s_red[4];
+  const uint32_t row = blockIdx.x;
+  const u32x4* r8 = reinterpret_cast<const u32x4*>(x + (size_t)row * in_dim);
+  // magnitudes as integer bits (bf16 bits << 16); NaN and infinities count as 0
+  auto fin = [](uint32_t h) {
+    const uint32_t b = (h << 16) & kAbsMask;
+    return b < kInfBits ? b : 0u;
+  };
+  uint32_t mb = 0;
+#pragma unroll 4
+  for (uint32_t c = threadIdx.x; c < in_dim / 8; c += 256) {
+    const u32x4 v = r8[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) mb = max(mb, max(fin(w[k] & 0xFFFFu), fin(w[k] >> 16)));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mb = max(mb, (uint32_t)__shfl_xor((int)mb, off));
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mb;
+  __syncthreads();
+  const float mx = __uint_as_float(max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3])));
+  const float inv = mx > 0.0f ? ldexpf(1.0f, min(14 - ilogbf(mx), 126)) : 1.0f;
+  if (threadIdx.x == 0) row_inv[row] = inv;
+  u32x4* const o8 = reinterpret_cast<u32x4*>(q + (size_t)row * in_dim);
+#pragma unroll 4
+  for (uint32_t c = threadIdx.x; c < in_dim / 8; c += 256) {
+    const u32x4 v = r8[c];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = pack2<false>(bf16_bits_to_float((uint16_t)w[k]) * inv,
+                          bf16_bits_to_float((uint16_t)(w[k] >> 16)) * inv);
+    o8[c] = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
 
@@ -737,7 +783,8 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
     if (e != hipSuccess) return e;
     x = xq;
     if (!w8a8) m *= 2;  // the staged head / tail rows
-  } else if (row_inv) {
+  } else if (w8a8) {
+    if (!row_inv || !xq) return hipErrorInvalidValue;
     const uint64_t chunks = (uint64_t)m * (in_dim / 8);
     const uint32_t blocks = (uint32_t)((chunks + 255) / 256 < 8192 ? (chunks + 255) / 256 : 8192);
     if (bf)
@@ -748,6 +795,15 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
       hipLaunchKernelGGL(iq2xxs_quantize_rows_kernel<false>, dim3(blocks), dim3(256), 0, stream,
                          static_cast<const uint16_t*>(x), m, in_dim, row_inv,
                          static_cast<uint16_t*>(xq));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    x = xq;
+  } else if (bf) {
+    // bf16 rows staged as scaled f16: the f16 GEMM with f16 weights
+    if (!row_inv || !xq) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(iq2xxs_scale_stage_bf16_rows_kernel, dim3(m), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), in_dim, const_cast<float*>(row_inv),
+                       static_cast<uint16_t*>(xq));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     x = xq;
@@ -769,12 +825,11 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
   a.ws_records = out_dim * a.bpr * kScalesPerBlock;
   a.split_blocks = 0;
   a.out_split = 0;
+  // every row set runs on f16 weights: f16 x as given, bf16 and f32 rows and
+  // W8A8's q staged as f16 (row_inv: the scale the epilogue divides by)
   if (x_dtype == 0 && !w8a8) return launch_gemm_shape<false, 2>(a, out_rows, partials, stream);
-  if (row_inv)
-    return bf ? launch_gemm_shape<true, 1>(a, out_rows, partials, stream)
-              : launch_gemm_shape<false, 1>(a, out_rows, partials, stream);
-  return bf ? launch_gemm_shape<true, 0>(a, out_rows, partials, stream)
-            : launch_gemm_shape<false, 0>(a, out_rows, partials, stream);
+  if (row_inv) return launch_gemm_shape<false, 1>(a, out_rows, partials, stream);
+  return launch_gemm_shape<false, 0>(a, out_rows, partials, stream);
 }
 
 }  // namespace cmk

@@ -45,22 +45,24 @@ hipError_t launch_iq2xxs_matmul_simple(const void* x, int x_dtype, uint32_t m, c
                                        uint32_t in_dim, const float* row_inv, int num_cus,
                                        hipStream_t stream);
 
-// Prefill matmul (MFMA GEMM, weights dequantised into LDS as f16/bf16);
+// Prefill matmul (MFMA GEMM, weights dequantised into LDS as f16);
 // x_dtype 0 (f32), 1 (f16) or 2 (bf16), on shapes where gemm_supported() holds
 // (in_dim % 8 == 0, x and weights below 2 GB).  Needs 16-byte aligned x and
 // weight_bytes and 2-byte aligned weight_scales.
 // With row_inv non-null the activations are first written to xq (16-byte
-// aligned) from v = x * row_inv[r], and each output row is divided by
+// aligned) as f16 from v = x * row_inv[r], and each output row is divided by
 // row_inv[r]:
-//  - w8a8: q = clamp(round_half_away(v), +-127) in x's half type (exact), inv
-//    from launch_iq2xxs_row_inv_scale; xq holds gemm_w8a8_scratch_bytes (f16 /
+//  - w8a8: q = clamp(round_half_away(v), +-127) (exact in f16), inv from
+//    launch_iq2xxs_row_inv_scale; xq holds gemm_w8a8_scratch_bytes (f16 /
 //    bf16 x) or gemm_f32_scratch_bytes(m, in_dim, true) (f32 x);
-//  - f32 x without w8a8: the launch writes row_inv[r] = 2^(14 - floor(log2
-//    max|x_r|)) itself (v exact); row r is staged as the f16 head rne(v) and
-//    tail rne(v - head), two GEMM rows whose
-//    products are summed in the epilogue; xq holds gemm_f32_scratch_bytes(m,
-//    in_dim, false), and gemm_supported must hold for 2m rows.
-// f32 x always needs row_inv and xq.
+//  - bf16 x without w8a8: the launch writes row_inv[r] = 2^(14 - floor(log2
+//    max|x_r|)) itself and stages v as f16 (exact); xq holds
+//    gemm_w8a8_scratch_bytes;
+//  - f32 x without w8a8: row_inv as for bf16; row r is staged as the f16 head
+//    rne(v) and tail rne(v - head), two GEMM rows whose products are summed in
+//    the epilogue; xq holds gemm_f32_scratch_bytes(m, in_dim, false), and
+//    gemm_supported must hold for 2m rows.
+// f32 and bf16 x always need row_inv and xq.
 bool gemm_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim);
 size_t gemm_w8a8_scratch_bytes(uint32_t m, uint32_t in_dim);
 size_t gemm_f32_scratch_bytes(uint32_t m, uint32_t in_dim, bool w8a8);

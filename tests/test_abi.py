@@ -170,8 +170,9 @@ def test_workspace_and_path_queries(cabi):
             == 256 + 64 * 4096 * 2 + 8 * 64 * 4096 * 4)
     # half x: partials only; 8 tiles of 128 x 1024, 32 blocks per row split in 16
     assert cabi.workspace_size(cabi.CMK_F16, 128, 1024, 8192) == 16 * 128 * 1024 * 4
-    # 256 tiles (the M=512 prefill shape) or too few blocks: no split
-    assert cabi.workspace_size(cabi.CMK_BF16, 17, 64, 320) == 0
+    # 256 tiles (the M=512 prefill shape) or too few blocks: no split; bf16
+    # rows are staged as scaled f16 (row scales + the rows) for f16 weights
+    assert cabi.workspace_size(cabi.CMK_BF16, 17, 64, 320) == 256 + 17 * 320 * 2
     # in_dim % 8 != 0 keeps f32 rows off the GEMM (portable path, no workspace)
     assert cabi.matmul_path(cabi.CMK_F32, 64, 300, 1001) == "gemv"
     assert cabi.workspace_size(cabi.CMK_F32, 64, 300, 1001) == 0
