@@ -97,12 +97,13 @@ struct RowsArgs {
 // two otherwise (the registers a 1024-thread workgroup leaves a wave: 128).
 template <class F>
 constexpr uint32_t rows_units(int rows, bool vec, bool w8a8) {
-  return rows == (w8a8 ? 8 : 4) && vec && sizeof(typename F::Unit) <= 20 ? 4 : 2;
+  return (w8a8 ? rows == 8 : rows <= 4) && vec && sizeof(typename F::Unit) <= 20 ? 4 : 2;
 }
 
 // F: the weight format (iq_rows_formats.h); XD: activation dtype (0 f32,
 // 1 f16, 2 bf16); kVecX: activations can be read as aligned 16-byte vectors;
-// kW8A8: int8 activations q (kRows 8 or 32); otherwise kRows is 4 or 8; at
+// kW8A8: int8 activations q (kRows 8 or 32); otherwise kRows is 2, 4 or 8
+// (the plane sums of kRows / 2 rows per lane folded in the epilogue); at
 // least m.
 template <class F, int XD, bool kVecX, bool kW8A8, int kRows>
 __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) {
@@ -183,9 +184,12 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
       const u32x4 v = lds_u4(xs_base + sub * kRows * 4);
       xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
       xs[2] = __uint_as_float(v.z); xs[3] = __uint_as_float(v.w);
-    } else {
+    } else if constexpr (kT == 2) {
       const u32x2 v = lds_u2(xs_base + sub * kRows * 4);
       xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
+    } else if constexpr (kT == 1) {
+      xs[0] = *reinterpret_cast<const __attribute__((address_space(3))) float*>(
+          static_cast<uintptr_t>(xs_base + sub * kRows * 4));
     }
   };
 
@@ -509,7 +513,7 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   if ((uint64_t)out_dim * bpr * F::kBlockBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)out_dim * bpr * F::kScaleBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)m * in_dim * esize > kOutOfRange - 4096) return false;
-  p->rows = w8a8 ? (m <= 8 ? 8 : 32) : (m <= 4 ? 4 : 8);
+  p->rows = w8a8 ? (m <= 8 ? 8 : 32) : (m <= 2 ? 2 : (m <= 4 ? 4 : 8));
   // activation rows digitised per slice (W8A8 digitises the m rows only)
   const uint64_t task_rows = w8a8 ? m : p->rows;
   const uint64_t n_rg = (out_dim + 31) / 32;
@@ -577,6 +581,7 @@ static hipError_t launch_rows_v(const RowsArgs& a, const RowsPlan& p, bool w8a8,
   if (w8a8)
     return p.rows == 8 ? launch_rows_t<F, XD, V, true, 8>(a, p, stream)
                        : launch_rows_t<F, XD, V, true, 32>(a, p, stream);
+  if (p.rows == 2) return launch_rows_t<F, XD, V, false, 2>(a, p, stream);
   return p.rows == 4 ? launch_rows_t<F, XD, V, false, 4>(a, p, stream)
                      : launch_rows_t<F, XD, V, false, 8>(a, p, stream);
 }
