@@ -114,6 +114,10 @@ __device__ __forceinline__ u32x2 lds_u2(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) u32x2*>(
       static_cast<uintptr_t>(addr));
 }
+__device__ __forceinline__ uint32_t lds_u16(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) uint16_t*>(
+      static_cast<uintptr_t>(addr));
+}
 __device__ __forceinline__ u32x4 lds_u4(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(
       static_cast<uintptr_t>(addr));

@@ -36,8 +36,11 @@
 // its units.  K is processed in slices of S super-blocks whose digits fit in
 // LDS next to the tables; a wave holds at most kU units per slice and
 // prefetches the next slice's unit into the registers of the one it has just
-// unpacked.  The waves of a row group add their partial sums in wave order,
-// so results are deterministic.
+// unpacked.  A slice's scale bytes (d and sub-scales) for the chunk's rows are
+// loaded coalesced with the slice's activations and staged in LDS, where the
+// units read them: a unit's own scale bytes are a few scattered bytes per row,
+// which cost more than the unit's codes.  The waves of a row group add their
+// partial sums in wave order, so results are deterministic.
 //
 // W8A8 (true int8).  The reference fake-quantises x per row (q / inv with q =
 // clamp(round(x * inv), +-127), iq2_matmul.metal:85-126) and multiplies in
@@ -87,6 +90,7 @@ struct RowsArgs {
   uint32_t wb_records, ws_records, x_records;  // bytes addressable by the buffer loads
   uint32_t plane_stride;                       // LDS bytes between digit planes
   uint32_t xdig_ofs, xsc_ofs, flag_ofs;        // LDS layout; partial sums reuse xdig
+  uint32_t sc_ofs;  // the K slice's scale bytes for the chunk's rows: [row][block][bytes]
   // Non-null: out = silu(gate) * (x . w), the gated MLP step in the epilogue
   // (gate: [m, out_dim] f32, the gate projection's output).
   const float* gate;
@@ -114,6 +118,10 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
   constexpr uint32_t kAcc = kT;
   static_assert(!kW8A8 || kRows == 8 || kRows == 32, "W8A8 runs 8 or 32 rows per launch");
   constexpr uint32_t kU = rows_units<F>(kRows, kVecX, kW8A8);
+  // scale staging: 2-byte tasks per thread (a chunk holds R * 32 rows and a
+  // slice S blocks, R * S <= 8 kU)
+  constexpr uint32_t kSH = F::kScaleBytes / 2;
+  constexpr uint32_t kScaleTasks = (32 * 8 * kU * kSH + kRowsThreads - 1) / kRowsThreads;
   uint8_t* xdig = lds + a.xdig_ofs;
   float* xsc = reinterpret_cast<float*>(lds + a.xsc_ofs);
   float* red = reinterpret_cast<float*>(lds + a.xdig_ofs);
@@ -283,6 +291,34 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     }
   };
 
+  // ---- scale bytes of slice s for the chunk's rows, in 2-byte tasks: loaded
+  // with the slice's activations (coalesced, unlike a unit's own scattered
+  // scale bytes), written to LDS after its digitisation
+  uint32_t crow0 = 0;  // first row of the current chunk
+  uint32_t sraw[kScaleTasks];
+  auto load_scales = [&](uint32_t s) {
+    const uint32_t sb0 = s << a.slice_shift;
+    const uint32_t per_row = kSH << a.slice_shift;  // 2-byte tasks per row and slice
+#pragma unroll
+    for (uint32_t k = 0; k < kScaleTasks; ++k) {
+      const uint32_t i = tid + k * kRowsThreads;
+      const uint32_t rl = (i >> a.slice_shift) / kSH;
+      const uint32_t w = i - rl * per_row;
+      const bool ok = s < a.nslices && rl < R * 32 && crow0 + rl < a.out_dim &&
+                      sb0 + w / kSH < a.bpr;
+      sraw[k] = __builtin_amdgcn_raw_buffer_load_b16(
+          rs, ok ? ((crow0 + rl) * a.bpr + sb0) * F::kScaleBytes + 2 * w : kOutOfRange, 0, 0);
+    }
+  };
+  auto stage_scales = [&]() {
+#pragma unroll
+    for (uint32_t k = 0; k < kScaleTasks; ++k) {
+      const uint32_t i = tid + k * kRowsThreads;
+      if (i < ((R * 32 * kSH) << a.slice_shift))
+        *reinterpret_cast<uint16_t*>(lds + a.sc_ofs + 2 * i) = (uint16_t)sraw[k];
+    }
+  };
+
   // ---- weight units: this wave's t-th unit of slice s is half-super-block
   // ul = wp + P * t of the slice (super-block s * S + ul / 2, half ul % 2);
   // lane (n, h) loads its half of row n's bytes of the unit
@@ -293,7 +329,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     const uint32_t ul = wp + P * t;
     const uint32_t row = row0 + n;
     const bool ok = s < a.nslices && ul < 2 * min(S, a.bpr - sb0) && row < a.out_dim;
-    q[t] = F::load(rw, rs, ok, row * a.bpr + sb0 + (ul >> 1), ul & 1, h);
+    q[t] = F::load(rw, ok, row * a.bpr + sb0 + (ul >> 1), ul & 1, h);
   };
 
   float acc[kAcc];
@@ -301,12 +337,14 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
   for (uint32_t chunk = blockIdx.x; chunk < a.nchunks; chunk += gridDim.x) {
     if (chunk != blockIdx.x) sync();  // the previous chunk's flags are read
     row0 = (chunk * R + rgl) * 32;
+    crow0 = chunk * R * 32;
     const uint32_t code = !tables_ready ? F::seed(tid) : 0u;
     if (tid == 0) *s_special = 0;
     // set-up loads ahead of the weights: the first slice's activations, then a
     // barrier (which does not wait for loads), so that every wave's activation
     // requests are queued before any weight request
     load_x(0);
+    load_scales(0);
     sync();
 #pragma unroll
     for (uint32_t t = 0; t < kRowsUnitsEarly && t < kU; ++t) issue_unit(0, t);
@@ -327,16 +365,20 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
         *reinterpret_cast<u32x4*>(xdig + zero_plane * a.plane_stride + 16 * tid) =
             u32x4{0, 0, 0, 0};
       digitize(s);
+      stage_scales();
       sync();
       const uint32_t sb0 = s << a.slice_shift;
       const uint32_t s_eff = min(S, a.bpr - sb0);
+      // this lane's row of the staged scale bytes
+      const uint32_t sc_row = a.sc_ofs + ((rgl * 32 + n) << a.slice_shift) * F::kScaleBytes;
 #pragma unroll
       for (uint32_t t = 0; t < kU; ++t) {
         // the first slice's later units: one more in flight per unit computed
         if (s == 0 && t + kRowsUnitsEarly < kU) issue_unit(0, t + kRowsUnitsEarly);
         const uint32_t ul = wp + P * t;
         if (ul >= 2 * s_eff) break;  // uniform
-        // the codes of the unit's 4 sub-blocks for this lane's row
+        // the codes of the unit's 4 sub-blocks for this lane's row, and its scales
+        F::fill_scales(q[t], sc_row + (ul >> 1) * F::kScaleBytes, ul & 1);
         const typename F::Words w = F::unpack(q[t]);
         const float dq = F::unit_scale(q[t]);
         // the registers are free: prefetch (none after the last slice)
@@ -397,7 +439,8 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     run_slice(0);
     for (uint32_t s = 1; s < a.nslices; ++s) {
       load_x(s);
-      sync();  // the previous slice's digits are consumed
+      load_scales(s);
+      sync();  // the previous slice's digits and scales are consumed
       run_slice(s);
     }
 
@@ -496,7 +539,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 struct RowsPlan {
   uint32_t rows;  // kRows
   uint32_t rg_shift, nchunks, grid, slice_shift, nslices, plane_stride;
-  uint32_t xdig_ofs, xsc_ofs, flag_ofs;
+  uint32_t xdig_ofs, xsc_ofs, flag_ofs, sc_ofs;
   size_t lds;
 };
 
@@ -546,7 +589,11 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
     p->xdig_ofs = F::kTableBytes;
     p->xsc_ofs = p->xdig_ofs + align16r(region);
     p->flag_ofs = p->xsc_ofs + (w8a8 ? 0u : align16r(S * 8 * p->rows * 4));
-    p->lds = p->flag_ofs + rows_flag_bytes(p->rows);
+    // the kernel stages the slice's scale bytes in 32 * 8 * units 2-byte
+    // tasks per scale-byte pair: R * S <= 8 units (the slice growth keeps it)
+    if ((1ull << rs) * S > 8 * units) return false;
+    p->sc_ofs = p->flag_ofs + rows_flag_bytes(p->rows);
+    p->lds = p->sc_ofs + align16r((1ull << rs) * 32 * S * F::kScaleBytes);
     if (p->lds <= kGemvLdsLimit) return true;
     if (ss == 0) return false;
   }
@@ -619,6 +666,7 @@ static hipError_t launch_rows_fmt(const void* x, int x_dtype, uint32_t m, const 
   a.xdig_ofs = p.xdig_ofs;
   a.xsc_ofs = p.xsc_ofs;
   a.flag_ofs = p.flag_ofs;
+  a.sc_ofs = p.sc_ofs;
   a.gate = gate;
   switch (x_dtype) {
     case 0: return vec ? launch_rows_v<F, 0, true>(a, p, w8a8, stream)

@@ -14,6 +14,12 @@
 // IQ2_S) run one v_mfma_i32_32x32x16_i8 per 16 columns ("half" formats); the
 // others one v_mfma_i32_32x32x32_i8 per 32-column sub-block.
 //
+// Scales: the kernel stages each K slice's scale bytes for the workgroup's
+// rows in LDS (coalesced), and fill_scales reads a unit's d and sub-scales
+// from there (`addr`: the LDS address of the row's block scales); loading
+// them per unit from global memory took one wave-wide load per field, each
+// touching 32 rows' lines for 2 bytes.
+//
 // Lane roles: lane l = 32 h + n holds weight row n of the unit.  In a
 // 32-column MFMA it supplies columns 16 h .. 16 h + 15 of the sub-block
 // (groups 2h and 2h+1 of 8 weights); in a 16-column MFMA of half hf it
@@ -128,14 +134,14 @@ struct RowsFmtXXS {
     }
   }
   // Lane (n, h) of unit `half` of super-block sb: pair 2 half + h of row.
-  __device__ static Unit load(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, bool ok,
-                              uint32_t blk, uint32_t half, uint32_t h) {
+  __device__ static Unit load(__amdgpu_buffer_rsrc_t rw, bool ok, uint32_t blk, uint32_t half,
+                              uint32_t h) {
     Unit u;
     const uint32_t off = ok ? blk * kBlockBytes + half * 32 + 16 * h : kOutOfRange;
     u.q = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kUnitLoad);
-    u.d = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? blk * kScaleBytes : kOutOfRange, 0, 0);
     return u;
   }
+  __device__ static void fill_scales(Unit& u, uint32_t addr, uint32_t) { u.d = lds_u16(addr); }
   // d times the factor that cancels the 2^27 of pair_scale
   __device__ static float unit_scale(const Unit& u) {
     return half_bits_to_float((uint16_t)u.d) * 0x1p-27f;
@@ -215,16 +221,18 @@ struct RowsFmtXS {
       store_sign_row<true>(lds, i, sign_mask(i), half * 8, 8);
     }
   }
-  __device__ static Unit load(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, bool ok,
-                              uint32_t blk, uint32_t half, uint32_t h) {
+  __device__ static Unit load(__amdgpu_buffer_rsrc_t rw, bool ok, uint32_t blk, uint32_t half,
+                              uint32_t h) {
     Unit u;
     const uint32_t off = ok ? blk * kBlockBytes + half * 32 + 16 * h : kOutOfRange;
     u.q = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, kUnitLoad);
-    const uint32_t so = ok ? blk * kScaleBytes : kOutOfRange;
-    u.d = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
-    u.s01 = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so + 2 + 4 * half : kOutOfRange, 0, 0);
-    u.s23 = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so + 4 + 4 * half : kOutOfRange, 0, 0);
     return u;
+  }
+  // d, then the scale bytes of sub-blocks 4 half .. 4 half + 3
+  __device__ static void fill_scales(Unit& u, uint32_t addr, uint32_t half) {
+    u.d = lds_u16(addr);
+    u.s01 = lds_u16(addr + 2 + 4 * half);
+    u.s23 = lds_u16(addr + 4 + 4 * half);
   }
   __device__ static float unit_scale(const Unit& u) {
     return half_bits_to_float((uint16_t)u.d);
@@ -309,8 +317,8 @@ struct RowsFmtS {
     const uint32_t b = tid >> 2;
     store_copies<16>(lds + 65536 + b * 128, b, byte_sign_mask(b), 4 * (tid & 3), 4);
   }
-  __device__ static Unit load(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, bool ok,
-                              uint32_t blk, uint32_t half, uint32_t h) {
+  __device__ static Unit load(__amdgpu_buffer_rsrc_t rw, bool ok, uint32_t blk, uint32_t half,
+                              uint32_t h) {
     Unit u;
     const uint32_t base = blk * kBlockBytes;
     u.qs = __builtin_amdgcn_raw_buffer_load_b64(
@@ -319,11 +327,12 @@ struct RowsFmtS {
         rw, ok ? base + 32 + 16 * half + 8 * h : kOutOfRange, 0, kUnitLoad);
     u.qh = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? base + 64 + 4 * half : kOutOfRange,
                                                 0, kUnitLoad);
-    const uint32_t so = ok ? blk * kScaleBytes : kOutOfRange;
-    u.d = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
-    u.s01 = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so + 2 + 4 * half : kOutOfRange, 0, 0);
-    u.s23 = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so + 4 + 4 * half : kOutOfRange, 0, 0);
     return u;
+  }
+  __device__ static void fill_scales(Unit& u, uint32_t addr, uint32_t half) {
+    u.d = lds_u16(addr);
+    u.s01 = lds_u16(addr + 2 + 4 * half);
+    u.s23 = lds_u16(addr + 4 + 4 * half);
   }
   __device__ static float unit_scale(const Unit& u) {
     return half_bits_to_float((uint16_t)u.d);
@@ -412,8 +421,8 @@ struct RowsFmtS3 {
       store_copies<16>(lds + 65536 + b * 128, b, byte_sign_mask(b), 8 * half, 8);
     }
   }
-  __device__ static Unit load(__amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs, bool ok,
-                              uint32_t blk, uint32_t half, uint32_t h) {
+  __device__ static Unit load(__amdgpu_buffer_rsrc_t rw, bool ok, uint32_t blk, uint32_t half,
+                              uint32_t h) {
     Unit u;
     const uint32_t base = blk * kBlockBytes;
     // (blocks are 8-byte aligned only: the 16 code bytes as two 8-byte loads)
@@ -426,10 +435,12 @@ struct RowsFmtS3 {
         rw, ok ? base + 72 + 16 * half + 8 * h : kOutOfRange, 0, kUnitLoad);
     u.qh = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? base + 64 + 4 * half : kOutOfRange,
                                                 0, kUnitLoad);
-    const uint32_t so = ok ? blk * kScaleBytes : kOutOfRange;
-    u.d = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, 0);
-    u.sc = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so + 2 + 2 * half : kOutOfRange, 0, 0);
     return u;
+  }
+  // d, then the scale byte of sub-blocks 4 half .. 4 half + 3 (two nibbles each)
+  __device__ static void fill_scales(Unit& u, uint32_t addr, uint32_t half) {
+    u.d = lds_u16(addr);
+    u.sc = lds_u16(addr + 2 + 2 * half);
   }
   // d * 8: the activation scales carry the 1/8 of the IQ2 formats' dl
   __device__ static float unit_scale(const Unit& u) {
