@@ -662,6 +662,59 @@ __global__ __launch_bounds__(256) void iq2xxs_scale_stage_f32_rows_kernel(
   }
 }
 
+// The same staging with the row held in registers between its maximum and
+// its split (read once): one 1024-thread workgroup per row, kV 16-byte
+// chunks per thread (in_dim <= 4096 kV), 8-byte stores of 4 halves.  Results
+// are those of iq2xxs_scale_stage_f32_rows_kernel bit for bit.
+template <int kV>
+__global__ __launch_bounds__(1024) void iq2xxs_stage_f32_rows_held_kernel(
+    const float* __restrict__ x, uint32_t in_dim, float* __restrict__ row_inv,
+    uint16_t* __restrict__ q) {
+  __shared__ float s_red[16];
+  const uint32_t row = blockIdx.x, tid = threadIdx.x;
+  const uint32_t n4 = in_dim / 4;
+  const float4* r4 = reinterpret_cast<const float4*>(x + (size_t)row * in_dim);
+  auto fin = [](float v) {
+    const uint32_t b = __float_as_uint(v) & kAbsMask;
+    return b < kInfBits ? b : 0u;
+  };
+  float4 v[kV];
+  uint32_t mb = 0;
+#pragma unroll
+  for (int j = 0; j < kV; ++j) {
+    const uint32_t c = tid + 1024u * j;
+    v[j] = c < n4 ? r4[c] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+    mb = max(mb, max(max(fin(v[j].x), fin(v[j].y)), max(fin(v[j].z), fin(v[j].w))));
+  }
+  float mx = __uint_as_float(mb);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  if ((tid & 63) == 0) s_red[tid >> 6] = mx;
+  __syncthreads();
+  mx = s_red[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) mx = fmaxf(mx, s_red[w]);
+  const float inv = mx > 0.0f ? ldexpf(1.0f, min(14 - ilogbf(mx), 126)) : 1.0f;
+  if (tid == 0) row_inv[row] = inv;
+  uint16_t* const head = q + (size_t)(2 * row) * in_dim;
+#pragma unroll
+  for (int j = 0; j < kV; ++j) {
+    const uint32_t c = tid + 1024u * j;
+    if (c >= n4) break;
+    const float e[4] = {v[j].x * inv, v[j].y * inv, v[j].z * inv, v[j].w * inv};
+    uint32_t oh[2], ot[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float h0 = (float)(_Float16)e[2 * k], h1 = (float)(_Float16)e[2 * k + 1];
+      oh[k] = pack2<false>(h0, h1);
+      ot[k] = pack2<false>(fin(e[2 * k]) ? e[2 * k] - h0 : 0.0f,
+                           fin(e[2 * k + 1]) ? e[2 * k + 1] - h1 : 0.0f);
+    }
+    *reinterpret_cast<uint2*>(head + c * 4) = make_uint2(oh[0], oh[1]);
+    *reinterpret_cast<uint2*>(head + in_dim + c * 4) = make_uint2(ot[0], ot[1]);
+  }
+}
+
 // The activations are loaded in 16-byte chunks that are wholly in or out of
 // range (in_dim % 8 == 0), and every buffer offset stays below
 // kGemmOutOfRange.
@@ -684,6 +737,24 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
        i += (uint64_t)gridDim.x * blockDim.x) {
     float v = part[i];
     for (uint32_t z = 1; z < splits; ++z) v += part[z * n + i];
+    out[i] = v;
+  }
+}
+
+// The same sum over 16-byte chunks (n4 = n / 4; 16-byte aligned buffers).
+__global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(const float4* __restrict__ part,
+                                                                 uint32_t splits, uint64_t n4,
+                                                                 float4* __restrict__ out) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    float4 v = part[i];
+    for (uint32_t z = 1; z < splits; ++z) {
+      const float4 w = part[z * n4 + i];
+      v.x += w.x;
+      v.y += w.y;
+      v.z += w.z;
+      v.w += w.w;
+    }
     out[i] = v;
   }
 }
@@ -754,6 +825,15 @@ static hipError_t launch_gemm_shape(GemmArgs a, uint32_t out_rows, float* partia
   const hipError_t e = p.wide ? launch_gemm_t<kBf16, 256, 112, kQ>(a, p.splits, stream)
                               : launch_gemm_t<kBf16, 128, 128, kQ>(a, p.splits, stream);
   if (e != hipSuccess || p.splits == 1) return e;
+  if (n % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(partials) % 16 == 0) {
+    const uint64_t want = (n / 4 + 255) / 256;
+    const uint32_t blocks = (uint32_t)(want < 4096 ? want : 4096);
+    hipLaunchKernelGGL(gemm_split_reduce4_kernel, dim3(blocks), dim3(256), 0, stream,
+                       reinterpret_cast<const float4*>(partials), p.splits, n / 4,
+                       reinterpret_cast<float4*>(out));
+    return hipGetLastError();
+  }
   const uint64_t want = (n + 255) / 256;
   const uint32_t blocks = (uint32_t)(want < 4096 ? want : 4096);
   hipLaunchKernelGGL(gemm_split_reduce_kernel, dim3(blocks), dim3(256), 0, stream, partials,
@@ -775,10 +855,28 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
       hipLaunchKernelGGL(iq2xxs_stage_f32_w8a8_kernel, dim3(blocks), dim3(256), 0, stream,
                          static_cast<const float*>(x), m, in_dim, row_inv,
                          static_cast<uint16_t*>(xq));
-    else
-      hipLaunchKernelGGL(iq2xxs_scale_stage_f32_rows_kernel, dim3(m), dim3(256), 0, stream,
-                         static_cast<const float*>(x), in_dim, const_cast<float*>(row_inv),
-                         static_cast<uint16_t*>(xq));
+    else {
+      // the row held in registers where it fits (up to 32768 columns)
+      const float* xf = static_cast<const float*>(x);
+      float* ri = const_cast<float*>(row_inv);
+      uint16_t* q16 = static_cast<uint16_t*>(xq);
+      const uint32_t n4 = in_dim / 4;
+      if (n4 <= 1024)
+        hipLaunchKernelGGL(iq2xxs_stage_f32_rows_held_kernel<1>, dim3(m), dim3(1024), 0, stream,
+                           xf, in_dim, ri, q16);
+      else if (n4 <= 2048)
+        hipLaunchKernelGGL(iq2xxs_stage_f32_rows_held_kernel<2>, dim3(m), dim3(1024), 0, stream,
+                           xf, in_dim, ri, q16);
+      else if (n4 <= 4096)
+        hipLaunchKernelGGL(iq2xxs_stage_f32_rows_held_kernel<4>, dim3(m), dim3(1024), 0, stream,
+                           xf, in_dim, ri, q16);
+      else if (n4 <= 8192)
+        hipLaunchKernelGGL(iq2xxs_stage_f32_rows_held_kernel<8>, dim3(m), dim3(1024), 0, stream,
+                           xf, in_dim, ri, q16);
+      else
+        hipLaunchKernelGGL(iq2xxs_scale_stage_f32_rows_kernel, dim3(m), dim3(256), 0, stream, xf,
+                           in_dim, ri, q16);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     x = xq;

@@ -161,6 +161,31 @@ def test_gemm_uneven_k_split_stops_at_row_end(pkg, oracle, inputs, dev):
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_gemm_k_split_workspace_garbage(pkg, inputs, dev, dtype):
+    """The k-split partials live in the caller's workspace: filled with 0xFF
+    bytes, and reused by a second call, it gives the same bits as a fresh
+    workspace (every partial is written before the split-order sum reads it)."""
+    m, out_dim, in_dim = 128, 1024, 8192  # eight 128 x 128 tiles, k split in 16
+    cabi = pkg.cabi
+    xd = cabi.CMK_F32 if dtype == torch.float32 else cabi.CMK_F16
+    assert cabi.matmul_path(xd, m, out_dim, in_dim) == "gemm"
+    need = cabi.workspace_size(xd, m, out_dim, in_dim)
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim, seed=21)
+    wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim, seed=22), dtype, dev)
+    ref = pkg.iq2_matmul(xt, wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs)
+    work = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)
+    for _ in range(2):
+        out = torch.full((m, out_dim), float("nan"), dtype=torch.float32, device=dev)
+        cabi.matmul_raw(xt.data_ptr(), xd, xt.numel(), m, wbt.data_ptr(), wbt.numel(),
+                        wst.data_ptr(), wst.numel(), out_dim, in_dim, out.data_ptr(),
+                        workspace_ptr=work.data_ptr(), workspace_bytes=need,
+                        stream=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+
+
 # BASELINE config 4 at M=128: q / o (8192 x 8192), gate / up (K=8192, N=28672)
 # and down (K=28672, N=8192); k / v (N=1024) are in test_gpu_parity.
 CONFIG4_M128 = [(8192, 8192), (28672, 8192), (8192, 28672)]
