@@ -71,8 +71,11 @@ constexpr uint32_t kRowsMaxTasks = 2;  // digitisation tasks per thread and slic
 // Units of the first slice issued before the set-up work (tables, digits); the
 // rest are issued one per computed unit.  A CU's memory pipeline stalls a wave
 // at issue while it is full, so weight requests issued ahead of a barrier
-// would hold every wave at that barrier until they drain.
-constexpr uint32_t kRowsUnitsEarly = 1;
+// would hold every wave at that barrier until they drain.  W8A8, whose set-up
+// (int8 rows, no digit planes) is shorter, takes two (0.4 us less at 4 and 8
+// rows; one more unit early did not help mode Off, and slowed IQ2_XS at M=1).
+template <bool kW8A8>
+constexpr uint32_t rows_units_early() { return kW8A8 ? 2 : 1; }
 // Flags and the W8A8 row scales.
 constexpr uint32_t rows_flag_bytes(uint32_t rows) { return (16 + 4 * rows + 15) & ~15u; }
 
@@ -118,6 +121,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
   constexpr uint32_t kAcc = kT;
   static_assert(!kW8A8 || kRows == 8 || kRows == 32, "W8A8 runs 8 or 32 rows per launch");
   constexpr uint32_t kU = rows_units<F>(kRows, kVecX, kW8A8);
+  constexpr uint32_t kEarly = rows_units_early<kW8A8>();
   // scale staging: 2-byte tasks per thread (a chunk holds R * 32 rows and a
   // slice S blocks, R * S <= 8 kU)
   constexpr uint32_t kSH = F::kScaleBytes / 2;
@@ -347,7 +351,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     load_scales(0);
     sync();
 #pragma unroll
-    for (uint32_t t = 0; t < kRowsUnitsEarly && t < kU; ++t) issue_unit(0, t);
+    for (uint32_t t = 0; t < kEarly && t < kU; ++t) issue_unit(0, t);
     if (!tables_ready) {
       F::tables(lds, tid, code);
       tables_ready = true;
@@ -374,7 +378,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 #pragma unroll
       for (uint32_t t = 0; t < kU; ++t) {
         // the first slice's later units: one more in flight per unit computed
-        if (s == 0 && t + kRowsUnitsEarly < kU) issue_unit(0, t + kRowsUnitsEarly);
+        if (s == 0 && t + kEarly < kU) issue_unit(0, t + kEarly);
         const uint32_t ul = wp + P * t;
         if (ul >= 2 * s_eff) break;  // uniform
         // the codes of the unit's 4 sub-blocks for this lane's row, and its scales
