@@ -302,7 +302,7 @@ def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
         res[name] = {"k": k, "n": n, "m": 1, "mean_launch_us": us, "alg_bytes_per_launch": alg,
                      "gbs": alg / (us * 1e-6) / 1e9,
                      "frac_of_hbm_peak": alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                     "kernel": f"cmk::iq_gemv_rows_kernel<cmk::{fmt}, 0, true, false, 2>",
+                     "kernel": f"cmk::iq_gemv_rows_kernel<cmk::{fmt}, 0, true, false, 2, 1>",
                      "launches": steps}
         log(f"[bench] {name}: {us:.2f} us per launch, {res[name]['gbs']:.1f} GB/s")
         del graph, calls, reps

@@ -67,7 +67,13 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kRowsWaves = 16;
 constexpr uint32_t kRowsThreads = kRowsWaves * 64;
-constexpr uint32_t kRowsMaxTasks = 2;  // digitisation tasks per thread and slice
+// Digitisation tasks (8 columns of one activation row) per thread and slice:
+// one where one suffices -- up to 4 rows, W8A8 up to 4 rows -- two otherwise.
+// A second slot costs a load and a digitisation per thread even when empty
+// (0.4-2 us at 4 rows); one slot for 8 rows would halve their slices (slower).
+constexpr uint32_t rows_tasks(uint32_t rows, bool w8a8, uint32_t m) {
+  return (w8a8 ? m <= 4 : rows <= 4) ? 1 : 2;
+}
 // Units of the first slice issued before the set-up work (tables, digits); the
 // rest are issued one per computed unit.  A CU's memory pipeline stalls a wave
 // at issue while it is full, so weight requests issued ahead of a barrier
@@ -111,8 +117,8 @@ constexpr uint32_t rows_units(int rows, bool vec, bool w8a8) {
 // 1 f16, 2 bf16); kVecX: activations can be read as aligned 16-byte vectors;
 // kW8A8: int8 activations q (kRows 8 or 32); otherwise kRows is 2, 4 or 8
 // (the plane sums of kRows / 2 rows per lane folded in the epilogue); at
-// least m.
-template <class F, int XD, bool kVecX, bool kW8A8, int kRows>
+// least m.  kTasks: digitisation task slots per thread (rows_tasks).
+template <class F, int XD, bool kVecX, bool kW8A8, int kRows, int kTasks>
 __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr uint32_t kT = kRows / 2;  // activation rows per lane: 2t + h
@@ -206,12 +212,12 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
   };
 
   // ---- digitisation of one K slice: task = row * (32 S) + 8-column group
-  XTask<XD, kVecX> xo[kRowsMaxTasks];
+  XTask<XD, kVecX> xo[kTasks];
   auto load_x = [&](uint32_t s) {
     const uint32_t sb0 = s << a.slice_shift;
     const uint32_t s_eff = min(S, a.bpr - sb0);
 #pragma unroll
-    for (uint32_t u = 0; u < kRowsMaxTasks; ++u) {
+    for (uint32_t u = 0; u < (uint32_t)kTasks; ++u) {
       const uint32_t task = u * kRowsThreads + tid;
       const uint32_t xrow = task >> (a.slice_shift + 5);
       const uint32_t col8 = task & (32 * S - 1);
@@ -224,7 +230,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     const uint32_t sb0 = s << a.slice_shift;
     const uint32_t s_eff = min(S, a.bpr - sb0);
 #pragma unroll
-    for (uint32_t u = 0; u < kRowsMaxTasks; ++u) {
+    for (uint32_t u = 0; u < (uint32_t)kTasks; ++u) {
       const uint32_t task = u * kRowsThreads + tid;
       const uint32_t xrow = task >> (a.slice_shift + 5);
       const uint32_t col8 = task & (32 * S - 1);
@@ -541,7 +547,8 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 // Launch policy.
 // ---------------------------------------------------------------------------
 struct RowsPlan {
-  uint32_t rows;  // kRows
+  uint32_t rows;   // kRows
+  uint32_t tasks;  // kTasks
   uint32_t rg_shift, nchunks, grid, slice_shift, nslices, plane_stride;
   uint32_t xdig_ofs, xsc_ofs, flag_ofs, sc_ofs;
   size_t lds;
@@ -561,6 +568,7 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   if ((uint64_t)out_dim * bpr * F::kScaleBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)m * in_dim * esize > kOutOfRange - 4096) return false;
   p->rows = w8a8 ? (m <= 8 ? 8 : 32) : (m <= 2 ? 2 : (m <= 4 ? 4 : 8));
+  p->tasks = rows_tasks(p->rows, w8a8, m);
   // activation rows digitised per slice (W8A8 digitises the m rows only)
   const uint64_t task_rows = w8a8 ? m : p->rows;
   const uint64_t n_rg = (out_dim + 31) / 32;
@@ -576,7 +584,7 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   const uint64_t units = rows_units<F>((int)p->rows, vec, w8a8);
   uint32_t ss = 0;
   while (2 * (2ull << ss) <= units * waves_per_rg &&
-         task_rows * (2ull << ss) * 32 <= kRowsMaxTasks * kRowsThreads &&
+         task_rows * (2ull << ss) * 32 <= p->tasks * kRowsThreads &&
          (1ull << ss) < bpr)
     ++ss;
   for (;; --ss) {
@@ -609,32 +617,35 @@ bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dt
   return plan_rows<RowsFmtXXS>(m, out_dim, in_dim, x_dtype, false, w8a8, 1, &p);
 }
 
-template <class F, int XD, bool V, bool Q, int ROWS>
+template <class F, int XD, bool V, bool Q, int ROWS, int TASKS>
 static hipError_t launch_rows_t(const RowsArgs& a, const RowsPlan& p, hipStream_t stream) {
   // The tables alone exceed the default 64 KB of dynamic LDS: raise the
   // limit once per instantiation.
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&iq_gemv_rows_kernel<F, XD, V, Q, ROWS>),
+        reinterpret_cast<const void*>(&iq_gemv_rows_kernel<F, XD, V, Q, ROWS, TASKS>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsLimit);
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
-  hipLaunchKernelGGL((iq_gemv_rows_kernel<F, XD, V, Q, ROWS>), dim3(p.grid), dim3(kRowsThreads),
-                     p.lds, stream, a);
+  hipLaunchKernelGGL((iq_gemv_rows_kernel<F, XD, V, Q, ROWS, TASKS>), dim3(p.grid),
+                     dim3(kRowsThreads), p.lds, stream, a);
   return hipGetLastError();
 }
 
 template <class F, int XD, bool V>
 static hipError_t launch_rows_v(const RowsArgs& a, const RowsPlan& p, bool w8a8,
                                 hipStream_t stream) {
-  if (w8a8)
-    return p.rows == 8 ? launch_rows_t<F, XD, V, true, 8>(a, p, stream)
-                       : launch_rows_t<F, XD, V, true, 32>(a, p, stream);
-  if (p.rows == 2) return launch_rows_t<F, XD, V, false, 2>(a, p, stream);
-  return p.rows == 4 ? launch_rows_t<F, XD, V, false, 4>(a, p, stream)
-                     : launch_rows_t<F, XD, V, false, 8>(a, p, stream);
+  // (task slots as rows_tasks chose them in the plan)
+  if (w8a8) {
+    if (p.rows == 32) return launch_rows_t<F, XD, V, true, 32, 2>(a, p, stream);
+    return p.tasks == 1 ? launch_rows_t<F, XD, V, true, 8, 1>(a, p, stream)
+                        : launch_rows_t<F, XD, V, true, 8, 2>(a, p, stream);
+  }
+  if (p.rows == 2) return launch_rows_t<F, XD, V, false, 2, 1>(a, p, stream);
+  return p.rows == 4 ? launch_rows_t<F, XD, V, false, 4, 1>(a, p, stream)
+                     : launch_rows_t<F, XD, V, false, 8, 2>(a, p, stream);
 }
 
 // One launch for m <= 8 rows (W8A8: m <= 32).
