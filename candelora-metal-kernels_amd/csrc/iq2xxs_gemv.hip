@@ -728,7 +728,7 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
 
 bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
   if (m > 1)
-    return gemv_rows_supported(m < 8 ? m : 8, out_dim, in_dim, x_dtype, false) &&
+    return gemv_rows_supported(m < 16 ? m : 16, out_dim, in_dim, x_dtype, false) &&
            gemv_rows_supported(m < 32 ? m : 32, out_dim, in_dim, x_dtype, true);
   GemvPlan p;
   return plan_gemv(m, out_dim, in_dim, x_dtype, 1, &p);
@@ -780,9 +780,9 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream, const float* gate) {
   if (m > 1) {
-    // groups of up to 8 activation rows (W8A8: 32), each decoding the weights once
+    // groups of up to 16 activation rows (W8A8: 32), each decoding the weights once
     const size_t esize = x_dtype == 0 ? 4 : 2;
-    const uint32_t group = w8a8 ? 32 : 8;
+    const uint32_t group = w8a8 ? 32 : 16;
     for (uint32_t r0 = 0; r0 < m; r0 += group) {
       const hipError_t e = launch_iq2xxs_gemv_rows(
           static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize, x_dtype,

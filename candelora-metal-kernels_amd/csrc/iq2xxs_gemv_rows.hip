@@ -1,10 +1,10 @@
-// iq2xxs_gemv_rows.hip — IQ2_XXS matmul for 2..8 activation rows (W8A8: up
-// to 32), and IQ2_XS, IQ2_S and IQ3_S matmuls for up to 8 rows per launch
+// iq2xxs_gemv_rows.hip — IQ2_XXS matmul for 2..16 activation rows (W8A8: up
+// to 32), and IQ2_XS, IQ2_S and IQ3_S matmuls for up to 16 rows per launch
 // (W8A8: 32), on gfx950.
 //
 // Replaces iq2_xxs_matmul_kernel / iq2_xxs_matmul_w8a8_kernel
 // (src/metal_src/iq2_matmul.metal:188-240, 436-499) for small m > 1, and the
-// IQ2_XS / IQ2_S / IQ3_S matmul kernels (:242-434, 501-699) for m <= 8 per
+// IQ2_XS / IQ2_S / IQ3_S matmul kernels (:242-434, 501-699) for m <= 16 per
 // launch.  The reference runs one thread per output, so every weight is
 // decoded once per activation row; here a weight is decoded once per launch
 // and one MFMA multiplies it against all the rows.  What differs between the
@@ -21,7 +21,8 @@
 // LDS tables ({g, -g} codebook rows, 8-byte sign masks, one bit select per
 // dword).  v_mfma_i32_32x32x32_i8 then takes
 //   A: 32 rows = 8 activation rows x 4 digit planes (plane 3 and absent rows
-//      read a zero plane), 32 columns = one sub-block;
+//      read a zero plane), 32 columns = one sub-block (16 activation rows:
+//      two such operands, each multiplied by the same decoded weights);
 //   B: the same 32 columns of 32 weight rows.
 // Lane l supplies A row l%32 and B column (weight row) l%32, both over columns
 // 16*(l/32) .. +15 of the sub-block (so A and B agree on the k order whatever
@@ -115,7 +116,7 @@ constexpr uint32_t rows_units(int rows, bool vec, bool w8a8) {
 
 // F: the weight format (iq_rows_formats.h); XD: activation dtype (0 f32,
 // 1 f16, 2 bf16); kVecX: activations can be read as aligned 16-byte vectors;
-// kW8A8: int8 activations q (kRows 8 or 32); otherwise kRows is 2, 4 or 8
+// kW8A8: int8 activations q (kRows 8 or 32); otherwise kRows is 2, 4, 8 or 16
 // (the plane sums of kRows / 2 rows per lane folded in the epilogue); at
 // least m.  kTasks: digitisation task slots per thread (rows_tasks).
 template <class F, int XD, bool kVecX, bool kW8A8, int kRows, int kTasks>
@@ -126,6 +127,10 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
   // 8 (r/4) + 4 h + r % 4), otherwise the plane sums folded into kT rows
   constexpr uint32_t kAcc = kT;
   static_assert(!kW8A8 || kRows == 8 || kRows == 32, "W8A8 runs 8 or 32 rows per launch");
+  // mode Off: 8 activation rows x 4 digit planes fill one A operand; 16 rows
+  // take two, multiplied by the same decoded weights
+  constexpr uint32_t kAOps = (!kW8A8 && kRows == 16) ? 2 : 1;
+  constexpr uint32_t kTO = kT / kAOps;  // activation-row pairs per A operand
   constexpr uint32_t kU = rows_units<F>(kRows, kVecX, kW8A8);
   constexpr uint32_t kEarly = rows_units_early<kW8A8>();
   // scale staging: 2-byte tasks per thread (a chunk holds R * 32 rows and a
@@ -192,16 +197,24 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
   // W8A8: A row l%32 = activation row l%32 (its q); rows from m on read zeros.
   const uint32_t ai = lane & 31, axr = ai >> 2, ap = ai & 3;
   const uint32_t zero_plane = kW8A8 ? a.m : 3u * kRows;
-  const uint32_t aplane = kW8A8 ? (ai < a.m ? ai : zero_plane)
-                                : ((ap == 3 || axr >= a.m) ? zero_plane : axr * 3 + ap);
-  const uint32_t a_base = a.xdig_ofs + aplane * a.plane_stride + (F::kHalf ? 8 : 16) * h;
+  uint32_t a_base[kAOps];
+#pragma unroll
+  for (uint32_t o = 0; o < kAOps; ++o) {
+    const uint32_t xr = axr + 8 * o;
+    const uint32_t aplane = kW8A8 ? (ai < a.m ? ai : zero_plane)
+                                  : ((ap == 3 || xr >= a.m) ? zero_plane : xr * 3 + ap);
+    a_base[o] = a.xdig_ofs + aplane * a.plane_stride + (F::kHalf ? 8 : 16) * h;
+  }
   const uint32_t xs_base = a.xsc_ofs + h * kT * 4;
   // activation scales of rows 2 tt + h for slice sub-block sub
   auto load_xs = [&](float* xs, uint32_t sub) {
-    if constexpr (kT == 4) {
-      const u32x4 v = lds_u4(xs_base + sub * kRows * 4);
-      xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
-      xs[2] = __uint_as_float(v.z); xs[3] = __uint_as_float(v.w);
+    if constexpr (kT >= 4) {
+#pragma unroll
+      for (uint32_t q4 = 0; q4 < kT / 4; ++q4) {
+        const u32x4 v = lds_u4(xs_base + sub * kRows * 4 + 16 * q4);
+        xs[4 * q4] = __uint_as_float(v.x); xs[4 * q4 + 1] = __uint_as_float(v.y);
+        xs[4 * q4 + 2] = __uint_as_float(v.z); xs[4 * q4 + 3] = __uint_as_float(v.w);
+      }
     } else if constexpr (kT == 2) {
       const u32x2 v = lds_u2(xs_base + sub * kRows * 4);
       xs[0] = __uint_as_float(v.x); xs[1] = __uint_as_float(v.y);
@@ -396,20 +409,21 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
         float au[kT];
 #pragma unroll
         for (uint32_t tt = 0; tt < kT; ++tt) au[tt] = 0.0f;
-        // c: this lane's 16 results of one MFMA; scale: the sub-scale of its
-        // columns.  Digits: au += (integer plane sums of c) * scale * xs,
-        // activation row 2 tt + h.  W8A8: acc += c * (2s+1) d, exact int32
-        // sums of q (|c| < 2^24) times an exact scale.
-        auto accumulate = [&](const v16i& c, float scale, const float* xs) {
+        // c: this lane's 16 results of the MFMA of A operand o; scale: the
+        // sub-scale of its columns.  Digits: au += (integer plane sums of c) *
+        // scale * xs, activation row 2 tt + h (tt = kTO o + i).  W8A8: acc +=
+        // c * (2s+1) d, exact int32 sums of q (|c| < 2^24) times an exact scale.
+        auto accumulate = [&](const v16i& c, float scale, const float* xs, uint32_t o) {
           if constexpr (kW8A8) {
             const float sd = scale * dq;
 #pragma unroll
             for (uint32_t r = 0; r < kAcc; ++r) acc[r] = fmaf((float)c[r], sd, acc[r]);
           } else {
 #pragma unroll
-            for (uint32_t tt = 0; tt < kT; ++tt) {
-              const uint32_t hi = ((uint32_t)c[4 * tt + 2] << 8) + (uint32_t)c[4 * tt + 1];
-              const float f = (float)(int)((hi << 8) + (uint32_t)c[4 * tt]);
+            for (uint32_t i = 0; i < kTO; ++i) {
+              const uint32_t tt = kTO * o + i;
+              const uint32_t hi = ((uint32_t)c[4 * i + 2] << 8) + (uint32_t)c[4 * i + 1];
+              const float f = (float)(int)((hi << 8) + (uint32_t)c[4 * i]);
               au[tt] = fmaf(f, scale * xs[tt], au[tt]);
             }
           }
@@ -419,23 +433,31 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
           const uint32_t sub = ul * 4 + j;  // sub-block in the slice
           if constexpr (!F::kHalf) {
             const v4i bw = F::pair(w, j, fk);
-            const u32x4 av = lds_u4(a_base + sub * 32);
-            const v4i aw = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
-            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bw, v16i{}, 0, 0, 0);
             float xs[kT];
             if constexpr (!kW8A8) load_xs(xs, sub);
-            accumulate(c, F::pair_scale(w, j, fk), xs);
+            const float ps = F::pair_scale(w, j, fk);
+#pragma unroll
+            for (uint32_t o = 0; o < kAOps; ++o) {
+              const u32x4 av = lds_u4(a_base[o] + sub * 32);
+              const v4i aw = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+              const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bw, v16i{}, 0, 0, 0);
+              accumulate(c, ps, xs, o);
+            }
           } else {
             float xs[kT];
             if constexpr (!kW8A8) load_xs(xs, sub);
 #pragma unroll
             for (uint32_t hf = 0; hf < 2; ++hf) {
               const u32x2 bw = F::group(w, j, hf, fk);
-              const u32x2 av = lds_u2(a_base + sub * 32 + 16 * hf);
-              const v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(
-                  (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bw.y << 32) | bw.x),
-                  v16i{}, 0, 0, 0);
-              accumulate(c, F::group_scale(w, j, hf), xs);
+              const float gs = F::group_scale(w, j, hf);
+#pragma unroll
+              for (uint32_t o = 0; o < kAOps; ++o) {
+                const u32x2 av = lds_u2(a_base[o] + sub * 32 + 16 * hf);
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+                    (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bw.y << 32) | bw.x),
+                    v16i{}, 0, 0, 0);
+                accumulate(c, gs, xs, o);
+              }
             }
           }
         }
@@ -561,13 +583,13 @@ static uint32_t align16r(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
 template <class F>
 static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, bool vec,
                       bool w8a8, int num_cus, RowsPlan* p) {
-  if (m < 1 || m > (w8a8 ? 32u : 8u) || out_dim == 0 || in_dim == 0) return false;
+  if (m < 1 || m > (w8a8 ? 32u : 16u) || out_dim == 0 || in_dim == 0) return false;
   const uint64_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t esize = x_dtype == 0 ? 4 : 2;
   if ((uint64_t)out_dim * bpr * F::kBlockBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)out_dim * bpr * F::kScaleBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)m * in_dim * esize > kOutOfRange - 4096) return false;
-  p->rows = w8a8 ? (m <= 8 ? 8 : 32) : (m <= 2 ? 2 : (m <= 4 ? 4 : 8));
+  p->rows = w8a8 ? (m <= 8 ? 8 : 32) : (m <= 2 ? 2 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16)));
   p->tasks = rows_tasks(p->rows, w8a8, m);
   // activation rows digitised per slice (W8A8 digitises the m rows only)
   const uint64_t task_rows = w8a8 ? m : p->rows;
@@ -644,11 +666,12 @@ static hipError_t launch_rows_v(const RowsArgs& a, const RowsPlan& p, bool w8a8,
                         : launch_rows_t<F, XD, V, true, 8, 2>(a, p, stream);
   }
   if (p.rows == 2) return launch_rows_t<F, XD, V, false, 2, 1>(a, p, stream);
+  if (p.rows == 16) return launch_rows_t<F, XD, V, false, 16, 2>(a, p, stream);
   return p.rows == 4 ? launch_rows_t<F, XD, V, false, 4, 1>(a, p, stream)
                      : launch_rows_t<F, XD, V, false, 8, 2>(a, p, stream);
 }
 
-// One launch for m <= 8 rows (W8A8: m <= 32).
+// One launch for m <= 16 rows (W8A8: m <= 32).
 template <class F>
 static hipError_t launch_rows_fmt(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                   const uint8_t* ws, float* out, uint32_t out_dim,
@@ -704,7 +727,8 @@ hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const
 template <class F>
 static bool variant_rows_fit(uint32_t out_dim, uint32_t in_dim, int x_dtype) {
   RowsPlan p;
-  return plan_rows<F>(8, out_dim, in_dim, x_dtype, false, false, 1, &p) &&
+  return plan_rows<F>(16, out_dim, in_dim, x_dtype, false, false, 1, &p) &&
+         plan_rows<F>(8, out_dim, in_dim, x_dtype, false, false, 1, &p) &&
          plan_rows<F>(4, out_dim, in_dim, x_dtype, true, false, 1, &p) &&
          plan_rows<F>(32, out_dim, in_dim, x_dtype, false, true, 1, &p);
 }
@@ -723,9 +747,9 @@ hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint3
                                   uint32_t out_dim, uint32_t in_dim, bool w8a8, int num_cus,
                                   hipStream_t stream) {
   const size_t esize = x_dtype == 0 ? 4 : 2;
-  // groups of 8 activation rows (W8A8: 32), each a launch that reads every
+  // groups of 16 activation rows (W8A8: 32), each a launch that reads every
   // weight once
-  const uint32_t group = w8a8 ? 32 : 8;
+  const uint32_t group = w8a8 ? 32 : 16;
   for (uint32_t r0 = 0; r0 < m; r0 += group) {
     const uint32_t mr = m - r0 < group ? m - r0 : group;
     const void* xr = static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize;

@@ -132,13 +132,19 @@ def test_rows_results_independent_of_other_rows(pkg, inputs, dev):
     assert torch.equal(a[:5], d[:5])
 
 
-def test_rows_sixteen_f32_rows_in_two_groups(pkg, oracle, inputs, dev):
-    """f32 x keeps the exact-weight GEMV up to 16 rows: two launches of 8."""
-    m, out_dim, in_dim = 13, 4096, 4096
+@pytest.mark.parametrize("m", [9, 13, 16])
+def test_rows_sixteen_f32_rows_in_one_launch(pkg, oracle, inputs, dev, m):
+    """f32 x keeps the exact-weight GEMV up to 16 rows, in one launch that
+    decodes every weight once (two A operands of 8 rows x 4 digit planes)."""
+    out_dim, in_dim = 4096, 4096
     assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim) == "gemv"
     wb, ws = inputs.synthetic_weights(out_dim, in_dim)
     xt = x_tensor(inputs.synthetic_x(m, in_dim), torch.float32, dev)
     y = _check(pkg, oracle, xt, wb, ws, out_dim, in_dim, dev)
-    y8 = pkg.iq2_matmul(xt[8:].contiguous(), to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+    # rows do not see each other: a row's result is the same with the other
+    # rows changed (the second operand's rows 8.. scaled)
+    x2 = xt.clone()
+    x2[8:] *= -3.0
+    y2 = pkg.iq2_matmul(x2, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
                         pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
-    assert np.array_equal(y[8:], y8)
+    assert np.array_equal(y[:8], y2[:8])

@@ -59,9 +59,10 @@ def _check(pkg, oracle, v, xt, wb, ws, out_dim, in_dim, dev, w8a8=False):
 
 @pytest.mark.parametrize("v", VARIANTS)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("m", [1, 2, 5, 8])
+@pytest.mark.parametrize("m", [1, 2, 5, 8, 12, 16, 21])
 def test_variant_rows_ragged_shapes(pkg, oracle, dev, v, dtype, m):
-    """1000 rows (the last 32-row group has 8), K = 2000 (a partial super-block)."""
+    """1000 rows (the last 32-row group has 8), K = 2000 (a partial super-block);
+    up to 16 activation rows per launch (21: a launch of 16 and one of 5)."""
     out_dim, in_dim = 1000, 2000
     wb, ws = random_weights(oracle, v, out_dim, in_dim, 31 * v + m)
     xt = to_dev(_x(m, in_dim, 10 * v + m), dev).to(dtype)
@@ -114,15 +115,15 @@ def test_variant_rows_w8a8(pkg, oracle, dev, v, m):
 
 
 @pytest.mark.parametrize("v", VARIANTS)
-def test_variant_rows_many_rows_in_groups_of_eight(pkg, oracle, dev, v):
-    """m = 21: launches of 8, 8 and 5 rows, each equal to the same rows
+def test_variant_rows_many_rows_in_groups_of_sixteen(pkg, oracle, dev, v):
+    """m = 21: launches of 16 and 5 rows, each equal to the same rows
     multiplied on their own."""
     m, out_dim, in_dim = 21, 640, 1536
     wb, ws = random_weights(oracle, v, out_dim, in_dim, 120 + v)
     x = _x(m, in_dim, 130 + v)
     y = _check(pkg, oracle, v, to_dev(x, dev), wb, ws, out_dim, in_dim, dev)
     wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
-    for r0, r1 in ((0, 8), (8, 16), (16, 21)):
+    for r0, r1 in ((0, 16), (16, 21)):
         yg = pkg.iq2_matmul(to_dev(x[r0:r1], dev), wbt, wst, out_dim, in_dim,
                             variant_enum(pkg, v)).cpu().numpy()
         assert np.array_equal(yg, y[r0:r1]), (r0, r1)
