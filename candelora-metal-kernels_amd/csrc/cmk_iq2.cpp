@@ -44,10 +44,12 @@ size_t bytes_per_block(int v) { return v == CMK_IQ2_XXS ? 64 : cmk::variant_byte
 size_t scales_per_block(int v) { return v == CMK_IQ2_XXS ? 2 : cmk::variant_scales_per_block(v); }
 
 // Largest m served by the GEMV family (above it: the MFMA GEMM).  The GEMV
-// multiplies exact weights; the GEMM rounds them to f16 / bf16, which costs
-// f32 activations the precision they carry, so f32 x keeps the GEMV up to 16
-// rows.  f16 / bf16 x switch at 8 rows, where the two are level in time.
-constexpr size_t kGemvMaxM = 8;
+// multiplies exact weights (the GEMM rounds them to f16) and takes up to 16
+// rows in one launch, which at 9-16 rows is also faster than the GEMM for
+// f16 / bf16 x at the decode shapes (K=4096: 18.9-19.9 against 23.1-27.9 us at
+// N=14336; K=8192, N=28672: 54 against 86 us), the one exception measured being
+// N=4096 (16.1 against 13.2 us at 16 rows).
+constexpr size_t kGemvMaxM = 16;
 constexpr size_t kGemvMaxMF32 = 16;
 // W8A8 activations are int8 on the multi-row kernel, 32 rows per launch: at
 // 24 to 32 rows it is level in time with the GEMM (which rounds the weights
@@ -526,9 +528,9 @@ int cmk_iq2_matmul_swiglu(const void* x, cmk_dtype x_dtype, size_t x_len, size_t
   if (choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x, weight_bytes, weight_scales,
                   false) != Path::Gemv)
     return fail(CMK_ERR_UNSUPPORTED,
-                "matmul_swiglu serves the decode-shaped kernels (m <= %zu for F32 x, <= %zu for "
-                "F16/BF16, aligned weights): use cmk_iq2_matmul and cmk_swiglu",
-                kGemvMaxMF32, kGemvMaxM);
+                "matmul_swiglu serves the decode-shaped kernels (m <= %zu, aligned weights): use "
+                "cmk_iq2_matmul and cmk_swiglu",
+                kGemvMaxM);
   int cus = 0;
   rc = current_cu_count(&cus);
   if (rc != CMK_OK) return rc;

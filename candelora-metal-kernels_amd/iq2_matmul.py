@@ -201,8 +201,8 @@ def iq2_matmul_swiglu(x, weight_bytes, weight_scales, out_dim, in_dim, gate):
     """silu(gate) * iq2_xxs_matmul(x, ...): the up projection of a gated MLP
     with the swiglu step in its epilogue, so the step needs no launch of its
     own.  Equal, bit for bit, to swiglu(gate, iq2_xxs_matmul(x, ...)).  gate is
-    F32 shaped like the output ([out_dim] or [m, out_dim]); m <= 16 for F32 x,
-    <= 8 for F16 / BF16.  No counterpart in the reference, whose callers
+    F32 shaped like the output ([out_dim] or [m, out_dim]); m <= 16.  No
+    counterpart in the reference, whose callers
     compose the MLP from candle ops."""
     if x.device.type != "cuda" or gate.device != x.device:
         raise Iq2MatmulError("matmul_swiglu requires x and gate on one HIP device")

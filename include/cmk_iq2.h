@@ -93,7 +93,7 @@ typedef enum cmk_act_quant_mode {
  * (:237-259) and x must hold at least m*in_dim elements.
  * Dimensions must be non-zero and fit in u32 (:210-212, :305-311).
  * `workspace` may be NULL when cmk_iq2_matmul_workspace_size reports 0.  The
- * MFMA GEMM (m > 8, in_dim % 8 == 0) needs one for W8A8, for f32 x (each row
+ * MFMA GEMM (m > 16, in_dim % 8 == 0) needs one for W8A8, for f32 x (each row
  * scaled by a power of two and staged as an f16 head / tail pair, so x keeps
  * about 22 bits) and for shapes too small to fill the GPU, whose k is split
  * (partials summed in a fixed order: results are the same on every run).
@@ -186,7 +186,7 @@ int cmk_swiglu(const float *gate, const float *up, size_t n, cmk_dtype out_dtype
  * f32, `gate_len` elements, not overlapping out).  Equal, bit for bit, to
  * cmk_iq2_matmul into a buffer u followed by cmk_swiglu(gate, u, F32): the
  * epilogue evaluates the same fp32 expression on the same sum.  Serves the
- * decode-shaped kernels only (m <= 16 for F32 x, m <= 8 for F16 / BF16, no
+ * decode-shaped kernels only (m <= 16, no
  * activation quantisation, weight_bytes 16-byte and weight_scales 2-byte
  * aligned); CMK_ERR_UNSUPPORTED otherwise.  No workspace.  No counterpart in
  * the reference, whose callers compose the MLP from candle ops.  Device

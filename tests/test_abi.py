@@ -150,7 +150,9 @@ def test_workspace_and_path_queries(cabi):
             == 2048 + 512 * 4096 * 2)
     assert cabi.workspace_size(cabi.CMK_F32, 1, 4096, 4096, mode=cabi.CMK_ACT_QUANT_OFF) == 0
     assert cabi.matmul_path(cabi.CMK_F16, 512, 14336, 4096) == "gemm"
-    assert cabi.matmul_path(cabi.CMK_BF16, 9, 14336, 4096) == "gemm"
+    assert cabi.matmul_path(cabi.CMK_BF16, 17, 14336, 4096) == "gemm"
+    assert cabi.matmul_path(cabi.CMK_BF16, 9, 14336, 4096) == "gemv"
+    assert cabi.matmul_path(cabi.CMK_F16, 16, 14336, 4096) == "gemv"
     assert cabi.matmul_path(cabi.CMK_F16, 8, 14336, 4096) == "gemv"
     assert cabi.matmul_path(cabi.CMK_F32, 1, 14336, 4096) == "gemv"
     # f32 rows keep the exact-weight GEMV up to 16 rows; beyond, they are

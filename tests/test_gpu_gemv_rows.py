@@ -132,14 +132,18 @@ def test_rows_results_independent_of_other_rows(pkg, inputs, dev):
     assert torch.equal(a[:5], d[:5])
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("m", [9, 13, 16])
-def test_rows_sixteen_f32_rows_in_one_launch(pkg, oracle, inputs, dev, m):
-    """f32 x keeps the exact-weight GEMV up to 16 rows, in one launch that
-    decodes every weight once (two A operands of 8 rows x 4 digit planes)."""
+def test_rows_sixteen_rows_in_one_launch(pkg, oracle, inputs, dev, dtype, m):
+    """Up to 16 rows take the exact-weight GEMV, in one launch that decodes
+    every weight once (two A operands of 8 rows x 4 digit planes)."""
     out_dim, in_dim = 4096, 4096
-    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim) == "gemv"
+    cd = {torch.float32: pkg.cabi.CMK_F32, torch.float16: pkg.cabi.CMK_F16,
+          torch.bfloat16: pkg.cabi.CMK_BF16}[dtype]
+    assert pkg.cabi.matmul_path(cd, m, out_dim, in_dim) == "gemv"
+    assert pkg.cabi.matmul_path(cd, 17, out_dim, in_dim) == "gemm"
     wb, ws = inputs.synthetic_weights(out_dim, in_dim)
-    xt = x_tensor(inputs.synthetic_x(m, in_dim), torch.float32, dev)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim), dtype, dev)
     y = _check(pkg, oracle, xt, wb, ws, out_dim, in_dim, dev)
     # rows do not see each other: a row's result is the same with the other
     # rows changed (the second operand's rows 8.. scaled)

@@ -108,8 +108,6 @@ def test_matmul_swiglu_equals_matmul_then_swiglu(pkg, inputs, dev, m, k, n, dtyp
     """The up projection with silu(gate) * u in its epilogue gives the same
     bits as the matmul followed by cmk_swiglu (one fp32 expression on the same
     sums)."""
-    if dtype == torch.float16 and m > 8:
-        pytest.skip("f16 x above 8 rows takes the MFMA GEMM")
     wu, su = inputs.synthetic_weights(n, k, seed=21)
     x = torch.from_numpy(inputs.synthetic_x(m, k, seed=22)).to(dev).to(dtype)
     gate = torch.from_numpy(inputs.synthetic_x(m, n, seed=23)).to(dev)

@@ -331,7 +331,7 @@ def test_gemm_w8a8_bf16_ragged(pkg, oracle, inputs, dev):
     assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
 
 
-# -------------------------------------------------- f32 rows on the GEMM (m > 8)
+# ------------------------------------------------- rows staged for the GEMM (m > 16)
 
 def test_gemm_bf16_rows_staged_as_f16(pkg, oracle, inputs, dev):
     """bf16 x on the GEMM: each row is scaled by the power of two that brings
