@@ -197,14 +197,13 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
   // W8A8: A row l%32 = activation row l%32 (its q); rows from m on read zeros.
   const uint32_t ai = lane & 31, axr = ai >> 2, ap = ai & 3;
   const uint32_t zero_plane = kW8A8 ? a.m : 3u * kRows;
-  uint32_t a_base[kAOps];
-#pragma unroll
-  for (uint32_t o = 0; o < kAOps; ++o) {
-    const uint32_t xr = axr + 8 * o;
-    const uint32_t aplane = kW8A8 ? (ai < a.m ? ai : zero_plane)
-                                  : ((ap == 3 || xr >= a.m) ? zero_plane : xr * 3 + ap);
-    a_base[o] = a.xdig_ofs + aplane * a.plane_stride + (F::kHalf ? 8 : 16) * h;
-  }
+  const uint32_t aplane = kW8A8 ? (ai < a.m ? ai : zero_plane)
+                                : ((ap == 3 || axr >= a.m) ? zero_plane : axr * 3 + ap);
+  const uint32_t a_base0 = a.xdig_ofs + aplane * a.plane_stride + (F::kHalf ? 8 : 16) * h;
+  // the second operand (16 rows): activation rows 8..15
+  const uint32_t aplane1 = (ap == 3 || axr + 8 >= a.m) ? zero_plane : (axr + 8) * 3 + ap;
+  const uint32_t a_base[2] = {a_base0,
+                              a.xdig_ofs + aplane1 * a.plane_stride + (F::kHalf ? 8 : 16) * h};
   const uint32_t xs_base = a.xsc_ofs + h * kT * 4;
   // activation scales of rows 2 tt + h for slice sub-block sub
   auto load_xs = [&](float* xs, uint32_t sub) {
@@ -431,17 +430,41 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
           const uint32_t sub = ul * 4 + j;  // sub-block in the slice
-          if constexpr (!F::kHalf) {
+          // (the one-operand instantiations keep their own code: written as the
+          // two-operand loop with one trip, the compiler schedules them
+          // differently, and W8A8 at 32 rows ran 8 % slower)
+          if constexpr (!F::kHalf && kAOps == 1) {
             const v4i bw = F::pair(w, j, fk);
+            const u32x4 av = lds_u4(a_base0 + sub * 32);
+            const v4i aw = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
+            const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bw, v16i{}, 0, 0, 0);
             float xs[kT];
             if constexpr (!kW8A8) load_xs(xs, sub);
-            const float ps = F::pair_scale(w, j, fk);
+            accumulate(c, F::pair_scale(w, j, fk), xs, 0);
+          } else if constexpr (!F::kHalf) {
+            const v4i bw = F::pair(w, j, fk);
+            float xs[kT];
 #pragma unroll
             for (uint32_t o = 0; o < kAOps; ++o) {
               const u32x4 av = lds_u4(a_base[o] + sub * 32);
               const v4i aw = {(int)av.x, (int)av.y, (int)av.z, (int)av.w};
               const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(aw, bw, v16i{}, 0, 0, 0);
-              accumulate(c, ps, xs, o);
+              if (o == 0) {
+                if constexpr (!kW8A8) load_xs(xs, sub);
+              }
+              accumulate(c, F::pair_scale(w, j, fk), xs, o);
+            }
+          } else if constexpr (kAOps == 1) {
+            float xs[kT];
+            if constexpr (!kW8A8) load_xs(xs, sub);
+#pragma unroll
+            for (uint32_t hf = 0; hf < 2; ++hf) {
+              const u32x2 bw = F::group(w, j, hf, fk);
+              const u32x2 av = lds_u2(a_base0 + sub * 32 + 16 * hf);
+              const v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(
+                  (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bw.y << 32) | bw.x),
+                  v16i{}, 0, 0, 0);
+              accumulate(c, F::group_scale(w, j, hf), xs, 0);
             }
           } else {
             float xs[kT];
@@ -449,14 +472,13 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 #pragma unroll
             for (uint32_t hf = 0; hf < 2; ++hf) {
               const u32x2 bw = F::group(w, j, hf, fk);
-              const float gs = F::group_scale(w, j, hf);
 #pragma unroll
               for (uint32_t o = 0; o < kAOps; ++o) {
                 const u32x2 av = lds_u2(a_base[o] + sub * 32 + 16 * hf);
                 const v16i c = __builtin_amdgcn_mfma_i32_32x32x16_i8(
                     (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bw.y << 32) | bw.x),
                     v16i{}, 0, 0, 0);
-                accumulate(c, gs, xs, o);
+                accumulate(c, F::group_scale(w, j, hf), xs, o);
               }
             }
           }
