@@ -60,6 +60,7 @@
 #include "iq2xxs_device.h"
 #include "iq2xxs_gemv_common.h"
 #include "iq2xxs_kernels.h"
+#include "iq_rows_formats.h"
 
 namespace cmk {
 
@@ -164,10 +165,20 @@ struct GemvArgs {
 // per thread per round; kW8A8: fake-quantise x per row first; kMulti: more
 // than one chunk per workgroup or more than one digitisation round (the loops
 // are compiled out otherwise).
-template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti>
+// kXS: IQ2_XS weights (the same 64 code bytes per block; 9-bit codebook
+// indices, a 4-bit sub-scale per 16 weights in 10 scale bytes per block): the
+// codebook rows of the multi-row kernel's IQ2_XS table, 8 copies of {g, -g}
+// per 128-byte row, the IQ2_XXS wide sign rows, four 16-column MFMA chains
+// per tile and 21-bit digits (16 x 2^21 x 43 < 2^31).  One chunk per
+// workgroup and dword-copied scales only.
+template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti, bool kXS = false>
 __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
+  static_assert(!kXS || (kWide && !kMulti), "IQ2_XS: wide tables, one chunk per workgroup");
   extern __shared__ __align__(16) uint8_t lds[];
   using TL = GemvTables<kWide>;
+  constexpr int kDS = kXS ? RowsFmtXS::kDigitShift : kDigitShift;  // digit bits
+  constexpr uint32_t kSB = kXS ? RowsFmtXS::kScaleBytes : kScalesPerBlock;  // scale bytes per block
+  constexpr uint32_t kSL = kXS ? 3 : kScaleLoads;  // staged scale dwords per thread
   // Tiles in flight ahead of the one computed.
   constexpr uint32_t kTilesAhead = 3;
   uint16_t* sscale = reinterpret_cast<uint16_t*>(lds + a.scale_ofs);
@@ -240,21 +251,21 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   };
   // Super-block scales of the chunk, staged as rows of a.spr entries (blocks
   // padded to whole slices) with zeros for padding rows and blocks.
-  uint32_t sraw[kScaleLoads];
+  uint32_t sraw[kSL];
   // (the looping kernels keep the 2-byte loads and the one-tile reductions:
   // they are at the 128-VGPR limit, and the alternatives cost spills)
   auto load_scales_of = [&](const ChunkGeom& g) {
     const uint32_t row_begin = g.row_begin, rows = g.rows;
     if (!kMulti && a.scale_dw) {
-      // a chunk's scales are contiguous and staged as they lie: rows*bpr/2
+      // a chunk's scales are contiguous and staged as they lie: rows*bpr*kSB/4
       // dwords (rows is a multiple of 4 or the chunk ends the matrix, and bpr is
       // then even); dwords past them read zeros
-      const uint32_t ndw = (rows * a.bpr + 1) / 2;
+      const uint32_t ndw = kXS ? (rows * a.bpr * kSB + 3) / 4 : (rows * a.bpr + 1) / 2;
 #pragma unroll
-      for (uint32_t k = 0; k < kScaleLoads; ++k) {
+      for (uint32_t k = 0; k < kSL; ++k) {
         const uint32_t t = tid + k * kGemvThreads;
         sraw[k] = __builtin_amdgcn_raw_buffer_load_b32(
-            rs, t < ndw ? row_begin * a.bpr * kScalesPerBlock + 4 * t : kOutOfRange, 0, 0);
+            rs, t < ndw ? row_begin * a.bpr * kSB + 4 * t : kOutOfRange, 0, 0);
       }
       return;
     }
@@ -272,9 +283,10 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     const uint32_t nstaged = a.rg_per_chunk * 4 * a.spr;
     if (!kMulti && a.scale_dw) {
 #pragma unroll
-      for (uint32_t k = 0; k < kScaleLoads; ++k) {
+      for (uint32_t k = 0; k < kSL; ++k) {
         const uint32_t t = tid + k * kGemvThreads;
-        if (2 * t < nstaged) reinterpret_cast<uint32_t*>(sscale)[t] = sraw[k];
+        if (kXS ? 4 * t < nstaged * kSB : 2 * t < nstaged)
+          reinterpret_cast<uint32_t*>(sscale)[t] = sraw[k];
       }
       return;
     }
@@ -372,7 +384,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         if ((task & 3) == 0) xsc[task >> 2] = 0.125f;
       } else if (task < a.ntasks) {
         const int e = digit_exponent(__uint_as_float(mb));
-        const float scale = ldexpf(1.0f, kDigitShift - e);
+        const float scale = ldexpf(1.0f, kDS - e);
         // biased digit bytes (each digit + 128), transposed into planes, then
         // the bias removed from four digits at a time
         uint32_t dg[8];
@@ -391,7 +403,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         *reinterpret_cast<uint2*>(xdig + c0) = make_uint2(p0[0], p0[1]);
         *reinterpret_cast<uint2*>(xdig + a.plane_stride + c0) = make_uint2(p1[0], p1[1]);
         *reinterpret_cast<uint2*>(xdig + 2 * a.plane_stride + c0) = make_uint2(p2[0], p2[1]);
-        if ((task & 3) == 0) xsc[task >> 2] = ldexpf(1.0f, e - kDigitShift - 3);
+        if ((task & 3) == 0) xsc[task >> 2] = ldexpf(1.0f, e - kDS - 3);
       }
     }
   };
@@ -419,6 +431,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 
   // ---- dot products of one tile
   const uint32_t cg = 16 * (lane & (TL::kGridCopies - 1));  // this lane's codebook copy
+  const uint32_t cg8 = 16 * (lane & 7);  // IQ2_XS: 8 codebook copies
   const uint32_t cs = TL::kSignBase + 8 * (lane & (TL::kSignCopies - 1));
   // Digit plane of this lane's A row.  Lanes with j = 3 load plane 2 as well:
   // A row 3 only feeds C row 3, which is never read, so its contents do not
@@ -430,6 +443,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   u32x4 q[kTilesPerWave];
   float acc[kTilesPerWave];
   float dsc[kTilesPerWave];  // d * 2^-27 of each tile's (row, pair); 0 when out of range
+  // IQ2_XS: d (no 2^-27), and the lane's two sub-scale bytes of each tile
+  uint32_t ssc[kXS ? kTilesPerWave : 1];
   // d of all of this wave's tiles, from the staged scales (one LDS round trip).
   // Staged entry of (row j, pair b): (rgl * 4) * spr + slice * 4 (uniform)
   // plus j * spr + b / 4 (this lane's constant).
@@ -440,7 +455,14 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (uint32_t k = 0; k < kTilesPerWave; ++k) {
       const uint32_t base = rgl * 4 * a.spr + slice * (kSlicePairs / 4);  // uniform
-      dsc[k] = k < cnt ? half_bits_to_float(sscale[base + scale_lane_ofs]) * 0x1p-27f : 0.0f;
+      if constexpr (kXS) {
+        // block (row, blk) at byte 10 * (row * bpr + blk) of the staged copy
+        const uint32_t ent = a.scale_ofs + kSB * (base + scale_lane_ofs);
+        dsc[k] = k < cnt ? half_bits_to_float(lds_u16(ent)) : 0.0f;
+        ssc[k] = lds_u16(ent + 2 + 2 * (b & 3));
+      } else {
+        dsc[k] = k < cnt ? half_bits_to_float(sscale[base + scale_lane_ofs]) * 0x1p-27f : 0.0f;
+      }
       if (++rgl == n_rg) {
         rgl = 0;
         ++slice;
@@ -467,6 +489,51 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       }
     }
     const uint32_t words[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
+    if constexpr (kXS) {
+      // sub-block h: u16 codes of groups 0, 1 in words[2h], of groups 2, 3 in
+      // words[2h + 1] (codebook index bits 0-8, ksigns index bits 9-15)
+      uint32_t w[2][8];
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        u32x4 gv[4];
+        u32x2 sm[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t word = words[2 * h + (g >> 1)];
+          const uint32_t sh = 16 * (g & 1);
+          gv[g] = lds_u4((__builtin_amdgcn_ubfe(word, sh, 9) << 7) | cg8);
+          sm[g] = lds_u2((__builtin_amdgcn_ubfe(word, sh + 9, 7) << 7) | cs);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          w[h][2 * g] = bit_select(sm[g].x, gv[g].z, gv[g].x);
+          w[h][2 * g + 1] = bit_select(sm[g].y, gv[g].w, gv[g].y);
+        }
+      }
+      // four chains: sub-block h, columns 16 q .. 16 q + 15 (a sub-scale each)
+      v4i c[2][2] = {{v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}}, {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}}};
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h)
+#pragma unroll
+          for (uint32_t qq = 0; qq < 2; ++qq)
+            c[h][qq] = mfma4x4((int)xr[h][4 * qq + kk], (int)w[h][4 * qq + kk], c[h][qq]);
+      // |plane sum| <= 16 * 43 * 2^21 < 2^31; dl = d * (2 s + 1) / 8 (the 1/8 is
+      // in the activation scale)
+      const uint32_t sc = ssc[k];
+      float r = 0.0f;
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        float t = 0.0f;
+#pragma unroll
+        for (uint32_t qq = 0; qq < 2; ++qq)
+          t = fmaf((float)plane_sum(c[h][qq]),
+                   (float)(2u * __builtin_amdgcn_ubfe(sc, 8 * h + 4 * qq, 4) + 1u), t);
+        r = fmaf(t * dsc[k], xs[h], r);
+      }
+      return r;
+    }
     // signed int8 weights of both sub-blocks: g where the mask is clear, -g where set
     uint32_t w[2][8];
 #pragma unroll
@@ -525,7 +592,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       if ((__float_as_uint(v) & kAbsMask) < kInfBits) continue;
       for (uint32_t rl = 0; rl < rows; ++rl)
         atomicOr(&s_kinds[rl],
-                 special_kind(v * iq2xxs_weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr)));
+                 special_kind(v * (kXS ? RowsFmtXS::weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr)
+                                       : iq2xxs_weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr))));
     }
     sync();
     for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
@@ -591,7 +659,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   uint32_t next = chunk + gridDim.x;
   ChunkGeom gn = geom_of(kMulti && next < a.nchunks ? next : chunk);
   // 1. set-up loads, ahead of every weight load
-  const uint32_t code = tid < 256 ? kGridCodesDev[tid] : 0u;
+  const uint32_t code = kXS ? RowsFmtXS::seed(tid) : (tid < 256 ? kGridCodesDev[tid] : 0u);
   if (tid == 0) *s_special = 0;
   load_scales();
   load_x(0, 0);
@@ -601,7 +669,9 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   for (uint32_t k = 0; k < kTilesEarly; ++k) q[k] = load_tile(k);
   __builtin_amdgcn_sched_barrier(0);
   // 3. tables (waves 0-7), digits (waves from 15 down), scales
-  if (tid < 256) {
+  if constexpr (kXS) {
+    RowsFmtXS::tables(lds, tid, code);
+  } else if (tid < 256) {
     store_grid_row<kWide>(lds, tid, code);
     if (!kWide) store_sign_row<kWide>(lds, tid, sign_mask(tid & 127), 0, TL::kSignCopies);
   } else if (kWide && tid < 512) {
@@ -680,8 +750,11 @@ static uint32_t align16(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
 
 // Launch shape for m x out_dim x in_dim on num_cus CUs; false when the shape
 // does not fit (LDS budget, 31-bit buffer offsets).
+// sb_bytes / scale_loads: scale bytes per block and staged scale dwords per
+// thread (IQ2_XS: 10 and 3).
 static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, int num_cus,
-                      GemvPlan* p) {
+                      GemvPlan* p, uint32_t sb_bytes = kScalesPerBlock,
+                      uint32_t scale_loads = kScaleLoads) {
   const uint64_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t npairs = bpr * 4;
   const uint64_t nsb = bpr * 8;
@@ -698,8 +771,14 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   const uint64_t per_wg_chunks = (target + rg_per_chunk - 1) / rg_per_chunk;
   rg_per_chunk = (target + per_wg_chunks - 1) / per_wg_chunks;
   const uint64_t spr = nslices * (kSlicePairs / 4);  // staged scales per row
-  if (rg_per_chunk * 4 * spr > (uint64_t)kScaleLoads * kGemvThreads) {
-    rg_per_chunk = (kScaleLoads * kGemvThreads) / (4 * spr);
+  if (sb_bytes == kScalesPerBlock) {
+    if (rg_per_chunk * 4 * spr > (uint64_t)scale_loads * kGemvThreads) {
+      rg_per_chunk = (scale_loads * kGemvThreads) / (4 * spr);
+      if (rg_per_chunk < 1) return false;
+    }
+  } else if (rg_per_chunk * 4 * spr * sb_bytes > (uint64_t)scale_loads * kGemvThreads * 4) {
+    // (the staged copy is rows * blocks * sb_bytes bytes, scale_loads dwords a thread)
+    rg_per_chunk = (scale_loads * kGemvThreads * 4) / (4 * spr * sb_bytes);
     if (rg_per_chunk < 1) return false;
   }
   p->nslices = (uint32_t)nslices;
@@ -711,7 +790,7 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   // longer rows digitise in further rounds
   p->xt = p->ntasks <= kGemvThreads ? 1 : 2;
   p->plane_stride = (uint32_t)(nsb * 32 + 16);
-  const uint64_t scale_bytes = align16(rg_per_chunk * 4 * nslices * (kSlicePairs / 4) * 2);
+  const uint64_t scale_bytes = align16(rg_per_chunk * 4 * nslices * (kSlicePairs / 4) * sb_bytes);
   const uint64_t rest = scale_bytes + align16(nsb * 4) + 3ull * p->plane_stride +
                         align16(rg_per_chunk * nslices * 16) + kGemvWaves * 4 + 16;
   p->wide = GemvTables<true>::kBytes + rest <= kGemvLdsLimit;
@@ -734,20 +813,20 @@ bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) 
   return plan_gemv(m, out_dim, in_dim, x_dtype, 1, &p);
 }
 
-template <int XD, bool V, bool W, int XT, bool Q, bool M>
+template <int XD, bool V, bool W, int XT, bool Q, bool M, bool XS = false>
 static hipError_t launch_gemv_t(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
   // The tables alone exceed the default 64 KB of dynamic LDS: raise the
   // limit once per instantiation.
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
-    hipError_t e =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&iq2xxs_gemv_kernel<XD, V, W, XT, Q, M>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsLimit);
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, XS>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsLimit);
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
-  hipLaunchKernelGGL((iq2xxs_gemv_kernel<XD, V, W, XT, Q, M>), dim3(p.grid), dim3(kGemvThreads),
-                     p.lds, stream, a);
+  hipLaunchKernelGGL((iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, XS>), dim3(p.grid),
+                     dim3(kGemvThreads), p.lds, stream, a);
   return hipGetLastError();
 }
 
@@ -776,24 +855,11 @@ static hipError_t launch_gemv_v(const GemvArgs& a, const GemvPlan& p, bool vec,
                 : launch_gemv_xt<XD, false, false>(a, p, stream);
 }
 
-hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
-                              const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              bool w8a8, int num_cus, hipStream_t stream, const float* gate) {
-  if (m > 1) {
-    // groups of up to 16 activation rows (W8A8: 32), each decoding the weights once
-    const size_t esize = x_dtype == 0 ? 4 : 2;
-    const uint32_t group = w8a8 ? 32 : 16;
-    for (uint32_t r0 = 0; r0 < m; r0 += group) {
-      const hipError_t e = launch_iq2xxs_gemv_rows(
-          static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize, x_dtype,
-          m - r0 < group ? m - r0 : group, wb, ws, out + (size_t)r0 * out_dim, out_dim, in_dim,
-          w8a8, num_cus, stream, gate ? gate + (size_t)r0 * out_dim : nullptr);
-      if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
-  }
-  GemvPlan p;
-  if (!plan_gemv(m, out_dim, in_dim, x_dtype, num_cus, &p)) return hipErrorInvalidValue;
+// The kernel arguments of a one-row launch planned as p (sb_bytes: scale
+// bytes per block).
+static GemvArgs gemv_args(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                          const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
+                          bool w8a8, const float* gate, const GemvPlan& p, uint32_t sb_bytes) {
   GemvArgs a;
   a.x = x;
   a.wb = wb;
@@ -812,7 +878,7 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
   a.nchunks = p.nchunks;
   a.ntasks = p.ntasks;
   a.wb_records = out_dim * a.bpr * kBytesPerBlock;
-  a.ws_records = out_dim * a.bpr * kScalesPerBlock;
+  a.ws_records = out_dim * a.bpr * sb_bytes;
   a.x_records = m * in_dim * (x_dtype == 0 ? 4u : 2u);
   a.plane_stride = p.plane_stride;
   a.scale_ofs = p.scale_ofs;
@@ -823,6 +889,75 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
   a.flag_ofs = p.flag_ofs;
   a.w8a8 = w8a8 ? 1 : 0;
   a.gate = gate;
+  return a;
+}
+
+// IQ2_XS at m = 1 on the one-row kernel: 16-byte aligned rows of x, 4-byte
+// aligned weight_scales, whole slices of 4 blocks per row, the wide tables,
+// one chunk per workgroup and one round of digits.
+static bool plan_gemv_xs(const void* x, const uint8_t* ws, uint32_t out_dim, uint32_t in_dim,
+                         int x_dtype, int num_cus, GemvPlan* p) {
+  const size_t esize = x_dtype == 0 ? 4 : 2;
+  const uint32_t bpr = (in_dim + kQK - 1) / kQK;
+  if (in_dim % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 ||
+      (size_t)in_dim * esize % 16 != 0 || reinterpret_cast<uintptr_t>(ws) % 4 != 0 ||
+      bpr % 4 != 0)
+    return false;
+  if ((uint64_t)out_dim * bpr * RowsFmtXS::kScaleBytes > kOutOfRange - 4096) return false;
+  if (!plan_gemv(1, out_dim, in_dim, x_dtype, num_cus, p, RowsFmtXS::kScaleBytes, 3)) return false;
+  return p->wide && p->nchunks <= p->grid && p->ntasks <= kGemvThreads * p->xt;
+}
+
+bool iq2xs_gemv_fits(const void* x, const uint8_t* ws, uint32_t out_dim, uint32_t in_dim,
+                     int x_dtype, int num_cus) {
+  GemvPlan p;
+  return plan_gemv_xs(x, ws, out_dim, in_dim, x_dtype, num_cus, &p);
+}
+
+template <int XD>
+static hipError_t launch_gemv_xs_xd(const GemvArgs& a, const GemvPlan& p, bool w8a8,
+                                    hipStream_t stream) {
+  if (w8a8)
+    return p.xt <= 1 ? launch_gemv_t<XD, true, true, 1, true, false, true>(a, p, stream)
+                     : launch_gemv_t<XD, true, true, 2, true, false, true>(a, p, stream);
+  return p.xt <= 1 ? launch_gemv_t<XD, true, true, 1, false, false, true>(a, p, stream)
+                   : launch_gemv_t<XD, true, true, 2, false, false, true>(a, p, stream);
+}
+
+hipError_t launch_iq2xs_gemv(const void* x, int x_dtype, const uint8_t* wb, const uint8_t* ws,
+                             float* out, uint32_t out_dim, uint32_t in_dim, bool w8a8,
+                             int num_cus, hipStream_t stream) {
+  GemvPlan p;
+  if (!plan_gemv_xs(x, ws, out_dim, in_dim, x_dtype, num_cus, &p)) return hipErrorInvalidValue;
+  const GemvArgs a = gemv_args(x, x_dtype, 1, wb, ws, out, out_dim, in_dim, w8a8, nullptr, p,
+                               RowsFmtXS::kScaleBytes);
+  switch (x_dtype) {
+    case 0: return launch_gemv_xs_xd<0>(a, p, w8a8, stream);
+    case 1: return launch_gemv_xs_xd<1>(a, p, w8a8, stream);
+    default: return launch_gemv_xs_xd<2>(a, p, w8a8, stream);
+  }
+}
+
+hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
+                              const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
+                              bool w8a8, int num_cus, hipStream_t stream, const float* gate) {
+  if (m > 1) {
+    // groups of up to 16 activation rows (W8A8: 32), each decoding the weights once
+    const size_t esize = x_dtype == 0 ? 4 : 2;
+    const uint32_t group = w8a8 ? 32 : 16;
+    for (uint32_t r0 = 0; r0 < m; r0 += group) {
+      const hipError_t e = launch_iq2xxs_gemv_rows(
+          static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize, x_dtype,
+          m - r0 < group ? m - r0 : group, wb, ws, out + (size_t)r0 * out_dim, out_dim, in_dim,
+          w8a8, num_cus, stream, gate ? gate + (size_t)r0 * out_dim : nullptr);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  GemvPlan p;
+  if (!plan_gemv(m, out_dim, in_dim, x_dtype, num_cus, &p)) return hipErrorInvalidValue;
+  const GemvArgs a = gemv_args(x, x_dtype, m, wb, ws, out, out_dim, in_dim, w8a8, gate, p,
+                               kScalesPerBlock);
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                    ((size_t)in_dim * esize % 16 == 0);

@@ -1,8 +1,10 @@
 """GPU parity of the IQ2_XS / IQ2_S / IQ3_S matmuls on the multi-row decode
-kernel (the one IQ2_XXS uses for 2..8 rows, with a format policy per variant).
+kernel (the one IQ2_XXS uses for 2..16 rows, with a format policy per variant),
+and of IQ2_XS at m = 1 on the one-row GEMV.
 
 With weight_bytes 16-byte and weight_scales 2-byte aligned, every m runs
-there, in launches of up to 8 activation rows.  The reference computes each
+there, in launches of up to 16 activation rows (IQ2_XS at m = 1 with K in
+whole 1024-column slices: the one-row GEMV).  The reference computes each
 output on its own (iq2_matmul.metal:242-434, 501-699), so the bar is the
 IQ2_XXS GEMV's: against the fp64 oracle product of the same x (W8A8: of the
 fake-quantised x), cond <= 1e-5 and rel <= 1e-3 (definitions in
@@ -158,3 +160,52 @@ def test_variant_rows_nonfinite_x(pkg, oracle, dev, v, pattern):
                                         out_dim, in_dim, wb, ws)
     cond, rel = errors(y[fin], y64[fin], sc[fin])
     assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+
+
+# ------------------------------------------- IQ2_XS at m = 1: the one-row GEMV
+# (its 64-byte code blocks fit that kernel's tiles; K in whole 1024-column
+# slices, 16-byte aligned x and 4-byte aligned weight_scales)
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("out_dim,in_dim", [(14336, 4096), (4096, 14336), (777, 3072)])
+def test_xs_one_row_vs_oracle(pkg, oracle, dev, dtype, out_dim, in_dim):
+    """BASELINE config 1's gate/up and down shapes, and a ragged row count."""
+    wb, ws = random_weights(oracle, XS, out_dim, in_dim, 160 + in_dim % 97)
+    xt = to_dev(_x(1, in_dim, 170 + out_dim % 89), dev).to(dtype)
+    _check(pkg, oracle, XS, xt, wb, ws, out_dim, in_dim, dev)
+
+
+def test_xs_one_row_w8a8(pkg, oracle, dev):
+    out_dim, in_dim = 2048, 4096
+    wb, ws = random_weights(oracle, XS, out_dim, in_dim, 181)
+    xt = to_dev(_x(1, in_dim, 182), dev)
+    _check(pkg, oracle, XS, xt, wb, ws, out_dim, in_dim, dev, w8a8=True)
+
+
+@pytest.mark.parametrize("pattern", ["nan", "posinf", "both_inf", "inf_and_nan"])
+def test_xs_one_row_nonfinite_x(pkg, oracle, dev, pattern):
+    """A NaN or an infinity in x at m = 1: output classes exactly the
+    oracle's (inf times a zero weight, d = 0, gives NaN)."""
+    m, out_dim, in_dim = 1, 1024, 4096
+    wb, ws = random_weights(oracle, XS, out_dim, in_dim, 190)
+    spb = oracle.scales_per_block(XS)
+    bpr = in_dim // 256
+    block = NONFINITE[pattern][0][0] // 256
+    zero_rows = [3, 17, out_dim - 1]
+    ws = ws.copy()
+    for r in zero_rows:
+        ws[spb * (r * bpr + block)] = 0
+        ws[spb * (r * bpr + block) + 1] = 0
+    x = _x(m, in_dim, 191)
+    for c, val in NONFINITE[pattern]:
+        x[0, c] = val
+    y = pkg.iq2_matmul(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       variant_enum(pkg, XS)).cpu().numpy()
+    ref = oracle.variant_matmul_reference(XS, x, m, out_dim, in_dim, wb, ws)
+    assert np.array_equal(classes(y), classes(ref)), pattern
+    fin = classes(ref) == 0
+    if fin.any():  # (a NaN in the only row makes every output NaN)
+        y64, sc = oracle.variant_matmul_f64(
+            XS, np.where(np.isfinite(x), x, 0.0).astype(np.float32), m, out_dim, in_dim, wb, ws)
+        cond, rel = errors(y[fin], y64[fin], sc[fin])
+        assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
