@@ -263,9 +263,11 @@ def bench_prefill(pkg, torch, stream, steps, warmup, m=512, k=4096, n=14336):
 
 
 # IQ2_XS, IQ2_S, IQ3_S: (ABI variant, bytes, scales per 256-weight block, the
-# format policy of the multi-row decode kernel that serves them)
-VARIANTS = [("iq2_xs", 1, 64, 10, "RowsFmtXS"), ("iq2_s", 2, 72, 10, "RowsFmtS"),
-            ("iq3_s", 3, 104, 6, "RowsFmtS3")]
+# kernel that serves them at M=1)
+VARIANTS = [("iq2_xs", 1, 64, 10,
+             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, true> (one-row GEMV, IQ2_XS)"),
+            ("iq2_s", 2, 72, 10, "cmk::iq_gemv_rows_kernel<cmk::RowsFmtS, 0, true, false, 2, 1>"),
+            ("iq3_s", 3, 104, 6, "cmk::iq_gemv_rows_kernel<cmk::RowsFmtS3, 0, true, false, 2, 1>")]
 
 
 def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
@@ -302,7 +304,7 @@ def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
         res[name] = {"k": k, "n": n, "m": 1, "mean_launch_us": us, "alg_bytes_per_launch": alg,
                      "gbs": alg / (us * 1e-6) / 1e9,
                      "frac_of_hbm_peak": alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                     "kernel": f"cmk::iq_gemv_rows_kernel<cmk::{fmt}, 0, true, false, 2, 1>",
+                     "kernel": fmt,
                      "launches": steps}
         log(f"[bench] {name}: {us:.2f} us per launch, {res[name]['gbs']:.1f} GB/s")
         del graph, calls, reps
