@@ -265,8 +265,9 @@ def bench_prefill(pkg, torch, stream, steps, warmup, m=512, k=4096, n=14336):
 # IQ2_XS, IQ2_S, IQ3_S: (ABI variant, bytes, scales per 256-weight block, the
 # kernel that serves them at M=1)
 VARIANTS = [("iq2_xs", 1, 64, 10,
-             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, true> (one-row GEMV, IQ2_XS)"),
-            ("iq2_s", 2, 72, 10, "cmk::iq_gemv_rows_kernel<cmk::RowsFmtS, 0, true, false, 2, 1>"),
+             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 1> (one-row GEMV, IQ2_XS)"),
+            ("iq2_s", 2, 72, 10,
+             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 2> (one-row GEMV, IQ2_S)"),
             ("iq3_s", 3, 104, 6, "cmk::iq_gemv_rows_kernel<cmk::RowsFmtS3, 0, true, false, 2, 1>")]
 
 
@@ -697,7 +698,7 @@ def main():
                      "traffic_source": ("profiles/gemv_config1_traffic.json: rocprofv3 FETCH_SIZE "
                                         "+ WRITE_SIZE per gate launch, copy-calibrated; read "
                                         "from the file, not measured in this run"),
-                     "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false> "
+                     "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false, 0> "
                                "(XT = 1 for K=4096, 2 for K=14336)",
                      "mean_launch_us": dec["mean_launch_us"],
                      "alg_bytes_per_launch": dec["per_launch_bytes"],

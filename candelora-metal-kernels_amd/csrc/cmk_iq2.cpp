@@ -324,13 +324,12 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
                             aligned(weight_scales, 2) &&
                             cmk::variant_rows_supported((int)variant, dims.out_dim, dims.in_dim,
                                                         (int)x_dtype);
-  // IQ2_XS at m = 1 takes the one-row GEMV where it fits (its 64-byte code
-  // blocks fit that kernel's tiles)
-  const bool xs_one_row = p == Path::Variant && variant == CMK_IQ2_XS && dims.m == 1 &&
-                          aligned(weight_bytes, 16) &&
-                          cmk::iq2xs_gemv_fits(x, weight_scales, dims.out_dim, dims.in_dim,
-                                               (int)x_dtype, cus);
-  if (row_inv && w8a8 && !variant_rows && !xs_one_row) {  // (f32 rows staged for the GEMM get their scales there)
+  // IQ2_XS and IQ2_S at m = 1 take the one-row GEMV where it fits
+  const bool variant_one_row = p == Path::Variant && dims.m == 1 &&
+                          (variant == CMK_IQ2_XS || variant == CMK_IQ2_S) &&
+                          cmk::iq_variant_gemv_fits((int)variant, x, weight_bytes, weight_scales,
+                                                    dims.out_dim, dims.in_dim, (int)x_dtype, cus);
+  if (row_inv && w8a8 && !variant_rows && !variant_one_row) {  // (f32 rows staged for the GEMM get their scales there)
     e = cmk::launch_iq2xxs_row_inv_scale(x, (int)x_dtype, dims.m, dims.in_dim, row_inv, s);
     if (e != hipSuccess) return hip_fail(e, "iq2_matmul row scale launch");
   }
@@ -350,9 +349,10 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
                                            out, dims.out_dim, dims.in_dim, row_inv, cus, s);
       break;
     case Path::Variant:
-      e = xs_one_row
-              ? cmk::launch_iq2xs_gemv(x, (int)x_dtype, weight_bytes, weight_scales, out,
-                                       dims.out_dim, dims.in_dim, w8a8, cus, s)
+      e = variant_one_row
+              ? cmk::launch_iq_variant_gemv((int)variant, x, (int)x_dtype, weight_bytes,
+                                            weight_scales, out, dims.out_dim, dims.in_dim, w8a8,
+                                            cus, s)
           : variant_rows
               ? cmk::launch_iq_variant_rows((int)variant, x, (int)x_dtype, dims.m, weight_bytes,
                                             weight_scales, out, dims.out_dim, dims.in_dim, w8a8,

@@ -165,20 +165,29 @@ struct GemvArgs {
 // per thread per round; kW8A8: fake-quantise x per row first; kMulti: more
 // than one chunk per workgroup or more than one digitisation round (the loops
 // are compiled out otherwise).
-// kXS: IQ2_XS weights (the same 64 code bytes per block; 9-bit codebook
-// indices, a 4-bit sub-scale per 16 weights in 10 scale bytes per block): the
-// codebook rows of the multi-row kernel's IQ2_XS table, 8 copies of {g, -g}
-// per 128-byte row, the IQ2_XXS wide sign rows, four 16-column MFMA chains
-// per tile and 21-bit digits (16 x 2^21 x 43 < 2^31).  One chunk per
-// workgroup and dword-copied scales only.
-template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti, bool kXS = false>
+// kFmt: the weight format.  kGemvXXS: IQ2_XXS.  kGemvXS: IQ2_XS (the same 64
+// code bytes per block; 9-bit codebook indices into the multi-row kernel's
+// IQ2_XS table, 8 copies of {g, -g} per 128-byte row, and the IQ2_XXS wide sign
+// rows).  kGemvS: IQ2_S (72 code bytes per block: grid low bytes, sign bytes
+// and 2 high index bits per group in three arrays, so a tile is three loads
+// per lane; the multi-row kernel's IQ2_S tables, 1024 rows x 4 copies and 256
+// sign-byte masks x 16 copies, 96 KB).  Both take a 4-bit sub-scale per 16
+// weights from 10 scale bytes per block, four 16-column MFMA chains per tile
+// and 21-bit digits (16 x 2^21 x 43 < 2^31), one chunk per workgroup and
+// dword-copied scales only.
+constexpr int kGemvXXS = 0, kGemvXS = 1, kGemvS = 2;
+
+template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti, int kFmt = kGemvXXS>
 __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
-  static_assert(!kXS || (kWide && !kMulti), "IQ2_XS: wide tables, one chunk per workgroup");
+  constexpr bool kXS = kFmt == kGemvXS, kS = kFmt == kGemvS;
+  constexpr bool kH16 = kXS || kS;  // a sub-scale per 16 weights, 10 scale bytes per block
+  static_assert(!kH16 || (kWide && !kMulti), "IQ2_XS / IQ2_S: wide tables, one chunk per workgroup");
   extern __shared__ __align__(16) uint8_t lds[];
   using TL = GemvTables<kWide>;
-  constexpr int kDS = kXS ? RowsFmtXS::kDigitShift : kDigitShift;  // digit bits
-  constexpr uint32_t kSB = kXS ? RowsFmtXS::kScaleBytes : kScalesPerBlock;  // scale bytes per block
-  constexpr uint32_t kSL = kXS ? 3 : kScaleLoads;  // staged scale dwords per thread
+  constexpr int kDS = kH16 ? RowsFmtXS::kDigitShift : kDigitShift;  // digit bits
+  constexpr uint32_t kSB = kH16 ? RowsFmtXS::kScaleBytes : kScalesPerBlock;  // scale bytes per block
+  constexpr uint32_t kSL = kH16 ? 3 : kScaleLoads;  // staged scale dwords per thread
+  constexpr uint32_t kLPT = kS ? 3 : 1;  // load instructions per tile
   // Tiles in flight ahead of the one computed.
   constexpr uint32_t kTilesAhead = 3;
   uint16_t* sscale = reinterpret_cast<uint16_t*>(lds + a.scale_ofs);
@@ -198,7 +207,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   const uint32_t b = lane >> 2;                  // 4x4 block of this lane
   const uint32_t j = lane & 3;                   // row in the row group / digit plane
   const uint32_t n_rg_total = (a.out_dim + 3) / 4;
-  const uint32_t row_bytes = a.bpr * kBytesPerBlock;
+  const uint32_t row_bytes = a.bpr * (kS ? RowsFmtS::kBlockBytes : kBytesPerBlock);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, a.x_records);
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.wb, a.wb_records);
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.ws, a.ws_records);
@@ -236,11 +245,27 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // past the buffer's end and read zeros; pairs past the row end read other
   // codes, whose staged scale d is 0; tiles past this wave's count are sent
   // past the buffer.
-  const uint32_t tile_lane_ofs = j * row_bytes + 16 * b;
+  const uint32_t tile_lane_ofs =
+      kS ? j * row_bytes + (b >> 2) * RowsFmtS::kBlockBytes + 8 * (b & 3) : j * row_bytes + 16 * b;
+  // IQ2_S: the 2 high-bit bytes of the lane's sub-blocks (the grid low bytes
+  // and the sign bytes are the tile's x, y and z, w)
+  uint32_t qhs[kS ? kTilesPerWave : 1];
   auto load_tile_of = [&](const ChunkGeom& g, uint32_t k) -> u32x4 {
     const uint32_t tau = g.t0 + k;
     const uint32_t slice = tau / g.n_rg;
     const uint32_t rgl = tau - slice * g.n_rg;
+    if constexpr (kS) {
+      const uint32_t base = k < g.cnt ? (g.row_begin + rgl * 4) * row_bytes +
+                                            slice * (kSlicePairs / 4) * RowsFmtS::kBlockBytes
+                                      : kOutOfRange;  // uniform
+      const u32x2 qs = __builtin_amdgcn_raw_buffer_load_b64(rw, base + tile_lane_ofs, 0,
+                                                            kStreamLoad);
+      const u32x2 sg = __builtin_amdgcn_raw_buffer_load_b64(rw, base + tile_lane_ofs + 32, 0,
+                                                            kStreamLoad);
+      qhs[k] = __builtin_amdgcn_raw_buffer_load_b16(
+          rw, base + tile_lane_ofs + 64 - 6 * (b & 3), 0, kStreamLoad);
+      return u32x4{qs.x, qs.y, sg.x, sg.y};
+    }
     const uint32_t base = k < g.cnt
                               ? (g.row_begin + rgl * 4) * row_bytes + slice * (kSlicePairs * 16)
                               : kOutOfRange;  // uniform
@@ -260,7 +285,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       // a chunk's scales are contiguous and staged as they lie: rows*bpr*kSB/4
       // dwords (rows is a multiple of 4 or the chunk ends the matrix, and bpr is
       // then even); dwords past them read zeros
-      const uint32_t ndw = kXS ? (rows * a.bpr * kSB + 3) / 4 : (rows * a.bpr + 1) / 2;
+      const uint32_t ndw = kH16 ? (rows * a.bpr * kSB + 3) / 4 : (rows * a.bpr + 1) / 2;
 #pragma unroll
       for (uint32_t k = 0; k < kSL; ++k) {
         const uint32_t t = tid + k * kGemvThreads;
@@ -285,7 +310,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (uint32_t k = 0; k < kSL; ++k) {
         const uint32_t t = tid + k * kGemvThreads;
-        if (kXS ? 4 * t < nstaged * kSB : 2 * t < nstaged)
+        if (kH16 ? 4 * t < nstaged * kSB : 2 * t < nstaged)
           reinterpret_cast<uint32_t*>(sscale)[t] = sraw[k];
       }
       return;
@@ -432,6 +457,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // ---- dot products of one tile
   const uint32_t cg = 16 * (lane & (TL::kGridCopies - 1));  // this lane's codebook copy
   const uint32_t cg8 = 16 * (lane & 7);  // IQ2_XS: 8 codebook copies
+  const uint32_t cg4 = 16 * (lane & 3);  // IQ2_S: 4 codebook copies
   const uint32_t cs = TL::kSignBase + 8 * (lane & (TL::kSignCopies - 1));
   // Digit plane of this lane's A row.  Lanes with j = 3 load plane 2 as well:
   // A row 3 only feeds C row 3, which is never read, so its contents do not
@@ -444,7 +470,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   float acc[kTilesPerWave];
   float dsc[kTilesPerWave];  // d * 2^-27 of each tile's (row, pair); 0 when out of range
   // IQ2_XS: d (no 2^-27), and the lane's two sub-scale bytes of each tile
-  uint32_t ssc[kXS ? kTilesPerWave : 1];
+  uint32_t ssc[kH16 ? kTilesPerWave : 1];
   // d of all of this wave's tiles, from the staged scales (one LDS round trip).
   // Staged entry of (row j, pair b): (rgl * 4) * spr + slice * 4 (uniform)
   // plus j * spr + b / 4 (this lane's constant).
@@ -455,7 +481,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (uint32_t k = 0; k < kTilesPerWave; ++k) {
       const uint32_t base = rgl * 4 * a.spr + slice * (kSlicePairs / 4);  // uniform
-      if constexpr (kXS) {
+      if constexpr (kH16) {
         // block (row, blk) at byte 10 * (row * bpr + blk) of the staged copy
         const uint32_t ent = a.scale_ofs + kSB * (base + scale_lane_ofs);
         dsc[k] = k < cnt ? half_bits_to_float(lds_u16(ent)) : 0.0f;
@@ -489,9 +515,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       }
     }
     const uint32_t words[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
-    if constexpr (kXS) {
-      // sub-block h: u16 codes of groups 0, 1 in words[2h], of groups 2, 3 in
-      // words[2h + 1] (codebook index bits 0-8, ksigns index bits 9-15)
+    if constexpr (kH16) {
       uint32_t w[2][8];
 #pragma unroll
       for (uint32_t h = 0; h < 2; ++h) {
@@ -499,10 +523,22 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         u32x2 sm[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const uint32_t word = words[2 * h + (g >> 1)];
-          const uint32_t sh = 16 * (g & 1);
-          gv[g] = lds_u4((__builtin_amdgcn_ubfe(word, sh, 9) << 7) | cg8);
-          sm[g] = lds_u2((__builtin_amdgcn_ubfe(word, sh + 9, 7) << 7) | cs);
+          if constexpr (kXS) {
+            // sub-block h: u16 codes of groups 0, 1 in words[2h], of groups 2, 3
+            // in words[2h + 1] (codebook index bits 0-8, ksigns index bits 9-15)
+            const uint32_t word = words[2 * h + (g >> 1)];
+            const uint32_t sh = 16 * (g & 1);
+            gv[g] = lds_u4((__builtin_amdgcn_ubfe(word, sh, 9) << 7) | cg8);
+            sm[g] = lds_u2((__builtin_amdgcn_ubfe(word, sh + 9, 7) << 7) | cs);
+          } else {
+            // sub-block h: grid low byte g of words[h], its 2 high bits at bit
+            // 2g of byte h of qhs[k]; sign byte g of words[2 + h] (rows of 16
+            // copies of its 8-byte mask at 64K)
+            const uint32_t idx = __builtin_amdgcn_ubfe(words[h], 8 * g, 8) |
+                                 (__builtin_amdgcn_ubfe(qhs[k], 8 * h + 2 * g, 2) << 8);
+            gv[g] = lds_u4((idx << 6) | cg4);
+            sm[g] = lds_u2((__builtin_amdgcn_ubfe(words[2 + h], 8 * g, 8) << 7) | cs);
+          }
         }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -593,7 +629,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       for (uint32_t rl = 0; rl < rows; ++rl)
         atomicOr(&s_kinds[rl],
                  special_kind(v * (kXS ? RowsFmtXS::weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr)
-                                       : iq2xxs_weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr))));
+                                   : kS ? RowsFmtS::weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr)
+                                        : iq2xxs_weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr))));
     }
     sync();
     for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
@@ -659,7 +696,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   uint32_t next = chunk + gridDim.x;
   ChunkGeom gn = geom_of(kMulti && next < a.nchunks ? next : chunk);
   // 1. set-up loads, ahead of every weight load
-  const uint32_t code = kXS ? RowsFmtXS::seed(tid) : (tid < 256 ? kGridCodesDev[tid] : 0u);
+  const uint32_t code = kXS ? RowsFmtXS::seed(tid)
+                            : kS ? RowsFmtS::seed(tid) : (tid < 256 ? kGridCodesDev[tid] : 0u);
   if (tid == 0) *s_special = 0;
   load_scales();
   load_x(0, 0);
@@ -671,6 +709,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // 3. tables (waves 0-7), digits (waves from 15 down), scales
   if constexpr (kXS) {
     RowsFmtXS::tables(lds, tid, code);
+  } else if constexpr (kS) {
+    RowsFmtS::tables(lds, tid, code);
   } else if (tid < 256) {
     store_grid_row<kWide>(lds, tid, code);
     if (!kWide) store_sign_row<kWide>(lds, tid, sign_mask(tid & 127), 0, TL::kSignCopies);
@@ -688,7 +728,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
   for (uint32_t k = kTilesEarly; k < kTilesAhead; ++k) q[k] = load_tile(k);
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kTilesAhead) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kTilesAhead * kLPT)
+               : "memory");
   __builtin_amdgcn_sched_barrier(0);
   // 4. once tile k has arrived, issue tile k + kTilesAhead, then compute tile k
   load_tile_scales();
@@ -697,6 +738,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   for (uint32_t k = 0; k < kTilesPerWave; ++k) {
     acc[k] = 0.0f;
     asm volatile("" ::"v"(q[k].x), "v"(q[k].y), "v"(q[k].z), "v"(q[k].w));
+    if constexpr (kS) asm volatile("" ::"v"(qhs[k]));
     __builtin_amdgcn_sched_barrier(0);
     if (k + kTilesAhead < kTilesPerWave) q[k + kTilesAhead] = load_tile(k + kTilesAhead);
     __builtin_amdgcn_sched_barrier(0);
@@ -752,9 +794,10 @@ static uint32_t align16(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
 // does not fit (LDS budget, 31-bit buffer offsets).
 // sb_bytes / scale_loads: scale bytes per block and staged scale dwords per
 // thread (IQ2_XS: 10 and 3).
+// table_bytes: a format's fixed table size (0: the IQ2_XXS wide or narrow layout).
 static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, int num_cus,
                       GemvPlan* p, uint32_t sb_bytes = kScalesPerBlock,
-                      uint32_t scale_loads = kScaleLoads) {
+                      uint32_t scale_loads = kScaleLoads, uint32_t table_bytes = 0) {
   const uint64_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t npairs = bpr * 4;
   const uint64_t nsb = bpr * 8;
@@ -793,8 +836,10 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   const uint64_t scale_bytes = align16(rg_per_chunk * 4 * nslices * (kSlicePairs / 4) * sb_bytes);
   const uint64_t rest = scale_bytes + align16(nsb * 4) + 3ull * p->plane_stride +
                         align16(rg_per_chunk * nslices * 16) + kGemvWaves * 4 + 16;
-  p->wide = GemvTables<true>::kBytes + rest <= kGemvLdsLimit;
-  const uint32_t tb = p->wide ? GemvTables<true>::kBytes : GemvTables<false>::kBytes;
+  p->wide = (table_bytes ? table_bytes : GemvTables<true>::kBytes) + rest <= kGemvLdsLimit;
+  if (table_bytes && !p->wide) return false;
+  const uint32_t tb =
+      table_bytes ? table_bytes : (p->wide ? GemvTables<true>::kBytes : GemvTables<false>::kBytes);
   p->scale_ofs = tb;
   p->xsc_ofs = p->scale_ofs + (uint32_t)scale_bytes;
   p->xdig_ofs = p->xsc_ofs + align16(nsb * 4);
@@ -813,19 +858,19 @@ bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) 
   return plan_gemv(m, out_dim, in_dim, x_dtype, 1, &p);
 }
 
-template <int XD, bool V, bool W, int XT, bool Q, bool M, bool XS = false>
+template <int XD, bool V, bool W, int XT, bool Q, bool M, int F = kGemvXXS>
 static hipError_t launch_gemv_t(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
   // The tables alone exceed the default 64 KB of dynamic LDS: raise the
   // limit once per instantiation.
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, XS>),
+        reinterpret_cast<const void*>(&iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, F>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsLimit);
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
-  hipLaunchKernelGGL((iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, XS>), dim3(p.grid),
+  hipLaunchKernelGGL((iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, F>), dim3(p.grid),
                      dim3(kGemvThreads), p.lds, stream, a);
   return hipGetLastError();
 }
@@ -859,7 +904,8 @@ static hipError_t launch_gemv_v(const GemvArgs& a, const GemvPlan& p, bool vec,
 // bytes per block).
 static GemvArgs gemv_args(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                           const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                          bool w8a8, const float* gate, const GemvPlan& p, uint32_t sb_bytes) {
+                          bool w8a8, const float* gate, const GemvPlan& p, uint32_t sb_bytes,
+                          uint32_t block_bytes = kBytesPerBlock) {
   GemvArgs a;
   a.x = x;
   a.wb = wb;
@@ -877,7 +923,7 @@ static GemvArgs gemv_args(const void* x, int x_dtype, uint32_t m, const uint8_t*
   a.rg_per_chunk = p.rg_per_chunk;
   a.nchunks = p.nchunks;
   a.ntasks = p.ntasks;
-  a.wb_records = out_dim * a.bpr * kBytesPerBlock;
+  a.wb_records = out_dim * a.bpr * block_bytes;
   a.ws_records = out_dim * a.bpr * sb_bytes;
   a.x_records = m * in_dim * (x_dtype == 0 ? 4u : 2u);
   a.plane_stride = p.plane_stride;
@@ -892,50 +938,67 @@ static GemvArgs gemv_args(const void* x, int x_dtype, uint32_t m, const uint8_t*
   return a;
 }
 
-// IQ2_XS at m = 1 on the one-row kernel: 16-byte aligned rows of x, 4-byte
-// aligned weight_scales, whole slices of 4 blocks per row, the wide tables,
-// one chunk per workgroup and one round of digits.
-static bool plan_gemv_xs(const void* x, const uint8_t* ws, uint32_t out_dim, uint32_t in_dim,
-                         int x_dtype, int num_cus, GemvPlan* p) {
+// IQ2_XS (variant 1) and IQ2_S (2) at m = 1 on the one-row kernel: 16-byte
+// aligned rows of x, weight_bytes 16-byte (IQ2_XS) or 8-byte (IQ2_S) and
+// weight_scales 4-byte aligned, whole slices of 4 blocks per row, the format's
+// tables, one chunk per workgroup and one round of digits.
+static bool plan_gemv_h16(int variant, const void* x, const uint8_t* wb, const uint8_t* ws,
+                          uint32_t out_dim, uint32_t in_dim, int x_dtype, int num_cus,
+                          GemvPlan* p) {
+  if (variant != 1 && variant != 2) return false;
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const uint32_t bpr = (in_dim + kQK - 1) / kQK;
+  const uint32_t block_bytes = variant == 1 ? RowsFmtXS::kBlockBytes : RowsFmtS::kBlockBytes;
   if (in_dim % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 ||
       (size_t)in_dim * esize % 16 != 0 || reinterpret_cast<uintptr_t>(ws) % 4 != 0 ||
-      bpr % 4 != 0)
+      reinterpret_cast<uintptr_t>(wb) % (variant == 1 ? 16 : 8) != 0 || bpr % 4 != 0)
     return false;
   if ((uint64_t)out_dim * bpr * RowsFmtXS::kScaleBytes > kOutOfRange - 4096) return false;
-  if (!plan_gemv(1, out_dim, in_dim, x_dtype, num_cus, p, RowsFmtXS::kScaleBytes, 3)) return false;
+  if ((uint64_t)out_dim * bpr * block_bytes > kOutOfRange - 4096) return false;
+  const uint32_t tables = variant == 1 ? RowsFmtXS::kTableBytes : RowsFmtS::kTableBytes;
+  if (!plan_gemv(1, out_dim, in_dim, x_dtype, num_cus, p, RowsFmtXS::kScaleBytes, 3, tables))
+    return false;
   return p->wide && p->nchunks <= p->grid && p->ntasks <= kGemvThreads * p->xt;
 }
 
-bool iq2xs_gemv_fits(const void* x, const uint8_t* ws, uint32_t out_dim, uint32_t in_dim,
-                     int x_dtype, int num_cus) {
+bool iq_variant_gemv_fits(int variant, const void* x, const uint8_t* wb, const uint8_t* ws,
+                          uint32_t out_dim, uint32_t in_dim, int x_dtype, int num_cus) {
   GemvPlan p;
-  return plan_gemv_xs(x, ws, out_dim, in_dim, x_dtype, num_cus, &p);
+  return plan_gemv_h16(variant, x, wb, ws, out_dim, in_dim, x_dtype, num_cus, &p);
 }
 
-template <int XD>
-static hipError_t launch_gemv_xs_xd(const GemvArgs& a, const GemvPlan& p, bool w8a8,
-                                    hipStream_t stream) {
+template <int XD, int F>
+static hipError_t launch_gemv_h16_xd(const GemvArgs& a, const GemvPlan& p, bool w8a8,
+                                     hipStream_t stream) {
   if (w8a8)
-    return p.xt <= 1 ? launch_gemv_t<XD, true, true, 1, true, false, true>(a, p, stream)
-                     : launch_gemv_t<XD, true, true, 2, true, false, true>(a, p, stream);
-  return p.xt <= 1 ? launch_gemv_t<XD, true, true, 1, false, false, true>(a, p, stream)
-                   : launch_gemv_t<XD, true, true, 2, false, false, true>(a, p, stream);
+    return p.xt <= 1 ? launch_gemv_t<XD, true, true, 1, true, false, F>(a, p, stream)
+                     : launch_gemv_t<XD, true, true, 2, true, false, F>(a, p, stream);
+  return p.xt <= 1 ? launch_gemv_t<XD, true, true, 1, false, false, F>(a, p, stream)
+                   : launch_gemv_t<XD, true, true, 2, false, false, F>(a, p, stream);
 }
 
-hipError_t launch_iq2xs_gemv(const void* x, int x_dtype, const uint8_t* wb, const uint8_t* ws,
-                             float* out, uint32_t out_dim, uint32_t in_dim, bool w8a8,
-                             int num_cus, hipStream_t stream) {
-  GemvPlan p;
-  if (!plan_gemv_xs(x, ws, out_dim, in_dim, x_dtype, num_cus, &p)) return hipErrorInvalidValue;
-  const GemvArgs a = gemv_args(x, x_dtype, 1, wb, ws, out, out_dim, in_dim, w8a8, nullptr, p,
-                               RowsFmtXS::kScaleBytes);
+template <int F>
+static hipError_t launch_gemv_h16_f(const GemvArgs& a, const GemvPlan& p, int x_dtype, bool w8a8,
+                                    hipStream_t stream) {
   switch (x_dtype) {
-    case 0: return launch_gemv_xs_xd<0>(a, p, w8a8, stream);
-    case 1: return launch_gemv_xs_xd<1>(a, p, w8a8, stream);
-    default: return launch_gemv_xs_xd<2>(a, p, w8a8, stream);
+    case 0: return launch_gemv_h16_xd<0, F>(a, p, w8a8, stream);
+    case 1: return launch_gemv_h16_xd<1, F>(a, p, w8a8, stream);
+    default: return launch_gemv_h16_xd<2, F>(a, p, w8a8, stream);
   }
+}
+
+hipError_t launch_iq_variant_gemv(int variant, const void* x, int x_dtype, const uint8_t* wb,
+                                  const uint8_t* ws, float* out, uint32_t out_dim,
+                                  uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream) {
+  GemvPlan p;
+  if (!plan_gemv_h16(variant, x, wb, ws, out_dim, in_dim, x_dtype, num_cus, &p))
+    return hipErrorInvalidValue;
+  const GemvArgs a =
+      gemv_args(x, x_dtype, 1, wb, ws, out, out_dim, in_dim, w8a8, nullptr, p,
+                RowsFmtXS::kScaleBytes,
+                variant == 1 ? RowsFmtXS::kBlockBytes : RowsFmtS::kBlockBytes);
+  return variant == 1 ? launch_gemv_h16_f<kGemvXS>(a, p, x_dtype, w8a8, stream)
+                      : launch_gemv_h16_f<kGemvS>(a, p, x_dtype, w8a8, stream);
 }
 
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,

@@ -90,14 +90,15 @@ hipError_t launch_iq_variant_matmul(int variant, const void* x, int x_dtype, uin
 // launches of up to 8 rows (W8A8: 32, int8 activations; row scales computed in
 // the kernel).  Needs
 // weight_bytes 16-byte and weight_scales 2-byte aligned.
-// IQ2_XS at m = 1 on the one-row GEMV (iq2xxs_gemv.hip): whether the launch
-// fits (alignment of x and weight_scales, K in whole 1024-column slices, one
-// chunk per workgroup), and the launch.
-bool iq2xs_gemv_fits(const void* x, const uint8_t* ws, uint32_t out_dim, uint32_t in_dim,
-                     int x_dtype, int num_cus);
-hipError_t launch_iq2xs_gemv(const void* x, int x_dtype, const uint8_t* wb, const uint8_t* ws,
-                             float* out, uint32_t out_dim, uint32_t in_dim, bool w8a8,
-                             int num_cus, hipStream_t stream);
+// IQ2_XS (variant 1) and IQ2_S (2) at m = 1 on the one-row GEMV
+// (iq2xxs_gemv.hip): whether the launch fits (alignment of x and the weight
+// buffers, K in whole 1024-column slices, one chunk per workgroup), and the
+// launch.
+bool iq_variant_gemv_fits(int variant, const void* x, const uint8_t* wb, const uint8_t* ws,
+                          uint32_t out_dim, uint32_t in_dim, int x_dtype, int num_cus);
+hipError_t launch_iq_variant_gemv(int variant, const void* x, int x_dtype, const uint8_t* wb,
+                                  const uint8_t* ws, float* out, uint32_t out_dim,
+                                  uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream);
 bool variant_rows_supported(int variant, uint32_t out_dim, uint32_t in_dim, int x_dtype);
 hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint32_t m,
                                   const uint8_t* wb, const uint8_t* ws, float* out,

@@ -1,10 +1,10 @@
 """GPU parity of the IQ2_XS / IQ2_S / IQ3_S matmuls on the multi-row decode
 kernel (the one IQ2_XXS uses for 2..16 rows, with a format policy per variant),
-and of IQ2_XS at m = 1 on the one-row GEMV.
+and of IQ2_XS and IQ2_S at m = 1 on the one-row GEMV.
 
 With weight_bytes 16-byte and weight_scales 2-byte aligned, every m runs
-there, in launches of up to 16 activation rows (IQ2_XS at m = 1 with K in
-whole 1024-column slices: the one-row GEMV).  The reference computes each
+there, in launches of up to 16 activation rows (IQ2_XS and IQ2_S at m = 1 with
+K in whole 1024-column slices: the one-row GEMV).  The reference computes each
 output on its own (iq2_matmul.metal:242-434, 501-699), so the bar is the
 IQ2_XXS GEMV's: against the fp64 oracle product of the same x (W8A8: of the
 fake-quantised x), cond <= 1e-5 and rel <= 1e-3 (definitions in
@@ -162,33 +162,36 @@ def test_variant_rows_nonfinite_x(pkg, oracle, dev, v, pattern):
     assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
 
 
-# ------------------------------------------- IQ2_XS at m = 1: the one-row GEMV
-# (its 64-byte code blocks fit that kernel's tiles; K in whole 1024-column
-# slices, 16-byte aligned x and 4-byte aligned weight_scales)
+# ---------------------------- IQ2_XS and IQ2_S at m = 1: the one-row GEMV
+# (K in whole 1024-column slices, 16-byte aligned x, weight_scales 4-byte and
+# weight_bytes 16-byte (IQ2_XS) / 8-byte (IQ2_S) aligned)
 
+@pytest.mark.parametrize("v", [XS, S])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("out_dim,in_dim", [(14336, 4096), (4096, 14336), (777, 3072)])
-def test_xs_one_row_vs_oracle(pkg, oracle, dev, dtype, out_dim, in_dim):
+def test_one_row_vs_oracle(pkg, oracle, dev, v, dtype, out_dim, in_dim):
     """BASELINE config 1's gate/up and down shapes, and a ragged row count."""
-    wb, ws = random_weights(oracle, XS, out_dim, in_dim, 160 + in_dim % 97)
+    wb, ws = random_weights(oracle, v, out_dim, in_dim, 160 + v + in_dim % 97)
     xt = to_dev(_x(1, in_dim, 170 + out_dim % 89), dev).to(dtype)
-    _check(pkg, oracle, XS, xt, wb, ws, out_dim, in_dim, dev)
+    _check(pkg, oracle, v, xt, wb, ws, out_dim, in_dim, dev)
 
 
-def test_xs_one_row_w8a8(pkg, oracle, dev):
+@pytest.mark.parametrize("v", [XS, S])
+def test_one_row_w8a8(pkg, oracle, dev, v):
     out_dim, in_dim = 2048, 4096
-    wb, ws = random_weights(oracle, XS, out_dim, in_dim, 181)
+    wb, ws = random_weights(oracle, v, out_dim, in_dim, 181 + v)
     xt = to_dev(_x(1, in_dim, 182), dev)
-    _check(pkg, oracle, XS, xt, wb, ws, out_dim, in_dim, dev, w8a8=True)
+    _check(pkg, oracle, v, xt, wb, ws, out_dim, in_dim, dev, w8a8=True)
 
 
+@pytest.mark.parametrize("v", [XS, S])
 @pytest.mark.parametrize("pattern", ["nan", "posinf", "both_inf", "inf_and_nan"])
-def test_xs_one_row_nonfinite_x(pkg, oracle, dev, pattern):
+def test_one_row_nonfinite_x(pkg, oracle, dev, v, pattern):
     """A NaN or an infinity in x at m = 1: output classes exactly the
     oracle's (inf times a zero weight, d = 0, gives NaN)."""
     m, out_dim, in_dim = 1, 1024, 4096
-    wb, ws = random_weights(oracle, XS, out_dim, in_dim, 190)
-    spb = oracle.scales_per_block(XS)
+    wb, ws = random_weights(oracle, v, out_dim, in_dim, 190 + v)
+    spb = oracle.scales_per_block(v)
     bpr = in_dim // 256
     block = NONFINITE[pattern][0][0] // 256
     zero_rows = [3, 17, out_dim - 1]
@@ -200,12 +203,30 @@ def test_xs_one_row_nonfinite_x(pkg, oracle, dev, pattern):
     for c, val in NONFINITE[pattern]:
         x[0, c] = val
     y = pkg.iq2_matmul(to_dev(x, dev), to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
-                       variant_enum(pkg, XS)).cpu().numpy()
-    ref = oracle.variant_matmul_reference(XS, x, m, out_dim, in_dim, wb, ws)
+                       variant_enum(pkg, v)).cpu().numpy()
+    ref = oracle.variant_matmul_reference(v, x, m, out_dim, in_dim, wb, ws)
     assert np.array_equal(classes(y), classes(ref)), pattern
     fin = classes(ref) == 0
     if fin.any():  # (a NaN in the only row makes every output NaN)
         y64, sc = oracle.variant_matmul_f64(
-            XS, np.where(np.isfinite(x), x, 0.0).astype(np.float32), m, out_dim, in_dim, wb, ws)
+            v, np.where(np.isfinite(x), x, 0.0).astype(np.float32), m, out_dim, in_dim, wb, ws)
         cond, rel = errors(y[fin], y64[fin], sc[fin])
+        assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+
+
+@pytest.mark.parametrize("v", [XS, S])
+def test_one_row_equals_its_own_row_in_a_pair(pkg, oracle, dev, v):
+    """The one-row GEMV (m = 1) and the multi-row kernel (m = 2) on the same
+    row agree to the GEMV bar (they sum in different orders)."""
+    out_dim, in_dim = 2048, 4096
+    wb, ws = random_weights(oracle, v, out_dim, in_dim, 200 + v)
+    x = _x(2, in_dim, 201)
+    wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
+    y1 = pkg.iq2_matmul(to_dev(x[:1], dev), wbt, wst, out_dim, in_dim,
+                        variant_enum(pkg, v)).cpu().numpy()
+    y2 = pkg.iq2_matmul(to_dev(x, dev), wbt, wst, out_dim, in_dim,
+                        variant_enum(pkg, v)).cpu().numpy()
+    y64, sc = oracle.variant_matmul_f64(v, x[:1], 1, out_dim, in_dim, wb, ws)
+    for y in (y1, y2[:1]):
+        cond, rel = errors(y, y64, sc)
         assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
