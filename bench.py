@@ -268,7 +268,8 @@ VARIANTS = [("iq2_xs", 1, 64, 10,
              "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 1> (one-row GEMV, IQ2_XS)"),
             ("iq2_s", 2, 72, 10,
              "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 2> (one-row GEMV, IQ2_S)"),
-            ("iq3_s", 3, 104, 6, "cmk::iq_gemv_rows_kernel<cmk::RowsFmtS3, 0, true, false, 2, 1>")]
+            ("iq3_s", 3, 104, 6,
+             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 3> (one-row GEMV, IQ3_S)")]
 
 
 def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):

@@ -324,9 +324,8 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
                             aligned(weight_scales, 2) &&
                             cmk::variant_rows_supported((int)variant, dims.out_dim, dims.in_dim,
                                                         (int)x_dtype);
-  // IQ2_XS and IQ2_S at m = 1 take the one-row GEMV where it fits
+  // IQ2_XS, IQ2_S and IQ3_S at m = 1 take the one-row GEMV where it fits
   const bool variant_one_row = p == Path::Variant && dims.m == 1 &&
-                          (variant == CMK_IQ2_XS || variant == CMK_IQ2_S) &&
                           cmk::iq_variant_gemv_fits((int)variant, x, weight_bytes, weight_scales,
                                                     dims.out_dim, dims.in_dim, (int)x_dtype, cus);
   if (row_inv && w8a8 && !variant_rows && !variant_one_row) {  // (f32 rows staged for the GEMM get their scales there)

@@ -174,20 +174,28 @@ struct GemvArgs {
 // sign-byte masks x 16 copies, 96 KB).  Both take a 4-bit sub-scale per 16
 // weights from 10 scale bytes per block, four 16-column MFMA chains per tile
 // and 21-bit digits (16 x 2^21 x 43 < 2^31), one chunk per workgroup and
-// dword-copied scales only.
-constexpr int kGemvXXS = 0, kGemvXS = 1, kGemvS = 2;
+// dword-copied scales only.  kGemvS3: IQ3_S (104 code bytes per block: two
+// 4-value entries per group, 9-bit indices from a low byte and one qh bit,
+// explicit sign bytes; four loads per lane per tile; the multi-row kernel's
+// IQ3_S tables, 512 rows x 16 copies of {g, -g} and the sign-byte masks, 96
+// KB), a sub-scale per 32 weights from 6 scale bytes per block, two chains per
+// tile as IQ2_XXS, dl = d (2s+1) and 21-bit digits (32 x 2^21 x 15 < 2^31).
+constexpr int kGemvXXS = 0, kGemvXS = 1, kGemvS = 2, kGemvS3 = 3;
 
 template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti, int kFmt = kGemvXXS>
 __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
-  constexpr bool kXS = kFmt == kGemvXS, kS = kFmt == kGemvS;
+  constexpr bool kXS = kFmt == kGemvXS, kS = kFmt == kGemvS, kS3 = kFmt == kGemvS3;
   constexpr bool kH16 = kXS || kS;  // a sub-scale per 16 weights, 10 scale bytes per block
-  static_assert(!kH16 || (kWide && !kMulti), "IQ2_XS / IQ2_S: wide tables, one chunk per workgroup");
+  constexpr bool kOther = kFmt != kGemvXXS;
+  static_assert(!kOther || (kWide && !kMulti), "other formats: wide tables, one chunk per workgroup");
   extern __shared__ __align__(16) uint8_t lds[];
   using TL = GemvTables<kWide>;
-  constexpr int kDS = kH16 ? RowsFmtXS::kDigitShift : kDigitShift;  // digit bits
-  constexpr uint32_t kSB = kH16 ? RowsFmtXS::kScaleBytes : kScalesPerBlock;  // scale bytes per block
-  constexpr uint32_t kSL = kH16 ? 3 : kScaleLoads;  // staged scale dwords per thread
-  constexpr uint32_t kLPT = kS ? 3 : 1;  // load instructions per tile
+  constexpr int kDS = kOther ? RowsFmtXS::kDigitShift : kDigitShift;  // digit bits
+  // scale bytes per block, and staged scale dwords per thread
+  constexpr uint32_t kSB =
+      kH16 ? RowsFmtXS::kScaleBytes : (kS3 ? RowsFmtS3::kScaleBytes : kScalesPerBlock);
+  constexpr uint32_t kSL = kH16 ? 3 : kScaleLoads;
+  constexpr uint32_t kLPT = kS ? 3 : (kS3 ? 4 : 1);  // load instructions per tile
   // Tiles in flight ahead of the one computed.
   constexpr uint32_t kTilesAhead = 3;
   uint16_t* sscale = reinterpret_cast<uint16_t*>(lds + a.scale_ofs);
@@ -207,7 +215,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   const uint32_t b = lane >> 2;                  // 4x4 block of this lane
   const uint32_t j = lane & 3;                   // row in the row group / digit plane
   const uint32_t n_rg_total = (a.out_dim + 3) / 4;
-  const uint32_t row_bytes = a.bpr * (kS ? RowsFmtS::kBlockBytes : kBytesPerBlock);
+  const uint32_t row_bytes =
+      a.bpr * (kS ? RowsFmtS::kBlockBytes : (kS3 ? RowsFmtS3::kBlockBytes : kBytesPerBlock));
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, a.x_records);
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.wb, a.wb_records);
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.ws, a.ws_records);
@@ -246,10 +255,13 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // codes, whose staged scale d is 0; tiles past this wave's count are sent
   // past the buffer.
   const uint32_t tile_lane_ofs =
-      kS ? j * row_bytes + (b >> 2) * RowsFmtS::kBlockBytes + 8 * (b & 3) : j * row_bytes + 16 * b;
+      kS    ? j * row_bytes + (b >> 2) * RowsFmtS::kBlockBytes + 8 * (b & 3)
+      : kS3 ? j * row_bytes + (b >> 2) * RowsFmtS3::kBlockBytes + 16 * (b & 3)
+            : j * row_bytes + 16 * b;
   // IQ2_S: the 2 high-bit bytes of the lane's sub-blocks (the grid low bytes
   // and the sign bytes are the tile's x, y and z, w)
-  uint32_t qhs[kS ? kTilesPerWave : 1];
+  uint32_t qhs[kS || kS3 ? kTilesPerWave : 1];
+  u32x2 sgs[kS3 ? kTilesPerWave : 1];  // IQ3_S: the sign bytes of the lane's sub-blocks
   auto load_tile_of = [&](const ChunkGeom& g, uint32_t k) -> u32x4 {
     const uint32_t tau = g.t0 + k;
     const uint32_t slice = tau / g.n_rg;
@@ -265,6 +277,18 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       qhs[k] = __builtin_amdgcn_raw_buffer_load_b16(
           rw, base + tile_lane_ofs + 64 - 6 * (b & 3), 0, kStreamLoad);
       return u32x4{qs.x, qs.y, sg.x, sg.y};
+    }
+    if constexpr (kS3) {
+      // (blocks are 8-byte aligned only: the 16 grid bytes as two 8-byte loads)
+      const uint32_t base = k < g.cnt ? (g.row_begin + rgl * 4) * row_bytes +
+                                            slice * (kSlicePairs / 4) * RowsFmtS3::kBlockBytes
+                                      : kOutOfRange;  // uniform
+      const uint32_t o = base + tile_lane_ofs;
+      const u32x2 q0 = __builtin_amdgcn_raw_buffer_load_b64(rw, o, 0, kStreamLoad);
+      const u32x2 q1 = __builtin_amdgcn_raw_buffer_load_b64(rw, o + 8, 0, kStreamLoad);
+      sgs[k] = __builtin_amdgcn_raw_buffer_load_b64(rw, o + 72 - 8 * (b & 3), 0, kStreamLoad);
+      qhs[k] = __builtin_amdgcn_raw_buffer_load_b16(rw, o + 64 - 14 * (b & 3), 0, kStreamLoad);
+      return u32x4{q0.x, q0.y, q1.x, q1.y};
     }
     const uint32_t base = k < g.cnt
                               ? (g.row_begin + rgl * 4) * row_bytes + slice * (kSlicePairs * 16)
@@ -285,7 +309,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       // a chunk's scales are contiguous and staged as they lie: rows*bpr*kSB/4
       // dwords (rows is a multiple of 4 or the chunk ends the matrix, and bpr is
       // then even); dwords past them read zeros
-      const uint32_t ndw = kH16 ? (rows * a.bpr * kSB + 3) / 4 : (rows * a.bpr + 1) / 2;
+      const uint32_t ndw = kOther ? (rows * a.bpr * kSB + 3) / 4 : (rows * a.bpr + 1) / 2;
 #pragma unroll
       for (uint32_t k = 0; k < kSL; ++k) {
         const uint32_t t = tid + k * kGemvThreads;
@@ -310,7 +334,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (uint32_t k = 0; k < kSL; ++k) {
         const uint32_t t = tid + k * kGemvThreads;
-        if (kH16 ? 4 * t < nstaged * kSB : 2 * t < nstaged)
+        if (kOther ? 4 * t < nstaged * kSB : 2 * t < nstaged)
           reinterpret_cast<uint32_t*>(sscale)[t] = sraw[k];
       }
       return;
@@ -458,6 +482,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   const uint32_t cg = 16 * (lane & (TL::kGridCopies - 1));  // this lane's codebook copy
   const uint32_t cg8 = 16 * (lane & 7);  // IQ2_XS: 8 codebook copies
   const uint32_t cg4 = 16 * (lane & 3);  // IQ2_S: 4 codebook copies
+  const uint32_t cs3 = 8 * (lane & 15);  // IQ3_S: 16 codebook copies of 8 bytes
   const uint32_t cs = TL::kSignBase + 8 * (lane & (TL::kSignCopies - 1));
   // Digit plane of this lane's A row.  Lanes with j = 3 load plane 2 as well:
   // A row 3 only feeds C row 3, which is never read, so its contents do not
@@ -470,7 +495,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   float acc[kTilesPerWave];
   float dsc[kTilesPerWave];  // d * 2^-27 of each tile's (row, pair); 0 when out of range
   // IQ2_XS: d (no 2^-27), and the lane's two sub-scale bytes of each tile
-  uint32_t ssc[kH16 ? kTilesPerWave : 1];
+  uint32_t ssc[kOther ? kTilesPerWave : 1];
   // d of all of this wave's tiles, from the staged scales (one LDS round trip).
   // Staged entry of (row j, pair b): (rgl * 4) * spr + slice * 4 (uniform)
   // plus j * spr + b / 4 (this lane's constant).
@@ -481,11 +506,14 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (uint32_t k = 0; k < kTilesPerWave; ++k) {
       const uint32_t base = rgl * 4 * a.spr + slice * (kSlicePairs / 4);  // uniform
-      if constexpr (kH16) {
-        // block (row, blk) at byte 10 * (row * bpr + blk) of the staged copy
+      if constexpr (kOther) {
+        // block (row, blk) at byte kSB * (row * bpr + blk) of the staged copy
         const uint32_t ent = a.scale_ofs + kSB * (base + scale_lane_ofs);
         dsc[k] = k < cnt ? half_bits_to_float(lds_u16(ent)) : 0.0f;
-        ssc[k] = lds_u16(ent + 2 + 2 * (b & 3));
+        // IQ2_XS / IQ2_S: the lane's two sub-scale bytes; IQ3_S: its byte (two
+        // nibbles), from an aligned 2-byte read
+        ssc[k] = kS3 ? lds_u16(ent + 2 + (b & 2)) >> (8 * (b & 1))
+                     : lds_u16(ent + 2 + 2 * (b & 3));
       } else {
         dsc[k] = k < cnt ? half_bits_to_float(sscale[base + scale_lane_ofs]) * 0x1p-27f : 0.0f;
       }
@@ -570,6 +598,43 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       }
       return r;
     }
+    if constexpr (kS3) {
+      // sub-block h: grid bytes in words[2h] (entries 0-3) and words[2h + 1]
+      // (entries 4-7), high index bits in byte h of qhs[k], sign bytes in
+      // sgs[k] word h; group l = entries 2l, 2l + 1 under sign byte l
+      uint32_t w[2][8];
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        const uint32_t sgw = h ? sgs[k].y : sgs[k].x;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+          const u32x2 m = lds_u2((__builtin_amdgcn_ubfe(sgw, 8 * l, 8) << 7) | cs);
+          u32x2 ge[2];
+#pragma unroll
+          for (int e2 = 0; e2 < 2; ++e2) {
+            const int e = 2 * l + e2;
+            const uint32_t idx = __builtin_amdgcn_ubfe(words[2 * h + (e >> 2)], 8 * (e & 3), 8) |
+                                 (__builtin_amdgcn_ubfe(qhs[k], 8 * h + e, 1) << 8);
+            ge[e2] = lds_u2((idx << 7) | cs3);
+          }
+          w[h][2 * l] = bit_select(m.x, ge[0].y, ge[0].x);
+          w[h][2 * l + 1] = bit_select(m.y, ge[1].y, ge[1].x);
+        }
+      }
+      v4i c[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        c[0] = mfma4x4((int)xr[0][kk], (int)w[0][kk], c[0]);
+        c[1] = mfma4x4((int)xr[1][kk], (int)w[1][kk], c[1]);
+      }
+      // |plane sum| <= 32 * 15 * 2^21 < 2^31; dl = d (2s+1), times 8 against the
+      // 1/8 the activation scales carry
+      const uint32_t sc = ssc[k];
+      const float d8 = dsc[k] * 8.0f;
+      const float t0 = (float)plane_sum(c[0]) * (float)(2u * (sc & 0xFu) + 1u);
+      const float t1 = (float)plane_sum(c[1]) * (float)(2u * ((sc >> 4) & 0xFu) + 1u);
+      return fmaf(t1 * d8, xs[1], (t0 * d8) * xs[0]);
+    }
     // signed int8 weights of both sub-blocks: g where the mask is clear, -g where set
     uint32_t w[2][8];
 #pragma unroll
@@ -630,7 +695,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         atomicOr(&s_kinds[rl],
                  special_kind(v * (kXS ? RowsFmtXS::weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr)
                                    : kS ? RowsFmtS::weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr)
-                                        : iq2xxs_weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr))));
+                                   : kS3 ? RowsFmtS3::weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr)
+                                         : iq2xxs_weight_at(a.wb, a.ws, row_begin + rl, c, a.bpr))));
     }
     sync();
     for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
@@ -697,7 +763,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   ChunkGeom gn = geom_of(kMulti && next < a.nchunks ? next : chunk);
   // 1. set-up loads, ahead of every weight load
   const uint32_t code = kXS ? RowsFmtXS::seed(tid)
-                            : kS ? RowsFmtS::seed(tid) : (tid < 256 ? kGridCodesDev[tid] : 0u);
+                        : kS ? RowsFmtS::seed(tid)
+                        : kS3 ? RowsFmtS3::seed(tid) : (tid < 256 ? kGridCodesDev[tid] : 0u);
   if (tid == 0) *s_special = 0;
   load_scales();
   load_x(0, 0);
@@ -711,6 +778,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     RowsFmtXS::tables(lds, tid, code);
   } else if constexpr (kS) {
     RowsFmtS::tables(lds, tid, code);
+  } else if constexpr (kS3) {
+    RowsFmtS3::tables(lds, tid, code);
   } else if (tid < 256) {
     store_grid_row<kWide>(lds, tid, code);
     if (!kWide) store_sign_row<kWide>(lds, tid, sign_mask(tid & 127), 0, TL::kSignCopies);
@@ -738,7 +807,8 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   for (uint32_t k = 0; k < kTilesPerWave; ++k) {
     acc[k] = 0.0f;
     asm volatile("" ::"v"(q[k].x), "v"(q[k].y), "v"(q[k].z), "v"(q[k].w));
-    if constexpr (kS) asm volatile("" ::"v"(qhs[k]));
+    if constexpr (kS || kS3) asm volatile("" ::"v"(qhs[k]));
+    if constexpr (kS3) asm volatile("" ::"v"(sgs[k].x), "v"(sgs[k].y));
     __builtin_amdgcn_sched_barrier(0);
     if (k + kTilesAhead < kTilesPerWave) q[k + kTilesAhead] = load_tile(k + kTilesAhead);
     __builtin_amdgcn_sched_barrier(0);
@@ -938,25 +1008,37 @@ static GemvArgs gemv_args(const void* x, int x_dtype, uint32_t m, const uint8_t*
   return a;
 }
 
-// IQ2_XS (variant 1) and IQ2_S (2) at m = 1 on the one-row kernel: 16-byte
-// aligned rows of x, weight_bytes 16-byte (IQ2_XS) or 8-byte (IQ2_S) and
-// weight_scales 4-byte aligned, whole slices of 4 blocks per row, the format's
-// tables, one chunk per workgroup and one round of digits.
+// Code and scale bytes per block of IQ2_XS (variant 1), IQ2_S (2), IQ3_S (3).
+static uint32_t variant_block_bytes(int v) {
+  return v == 1 ? RowsFmtXS::kBlockBytes : (v == 2 ? RowsFmtS::kBlockBytes : RowsFmtS3::kBlockBytes);
+}
+static uint32_t variant_scale_bytes(int v) {
+  return v == 3 ? RowsFmtS3::kScaleBytes : RowsFmtXS::kScaleBytes;
+}
+
+// IQ2_XS, IQ2_S and IQ3_S at m = 1 on the one-row kernel: 16-byte aligned rows
+// of x, weight_bytes 16-byte (IQ2_XS) or 8-byte aligned and weight_scales
+// 4-byte aligned, whole slices of 4 blocks per row, the format's tables, one
+// chunk per workgroup and one round of digits.
 static bool plan_gemv_h16(int variant, const void* x, const uint8_t* wb, const uint8_t* ws,
                           uint32_t out_dim, uint32_t in_dim, int x_dtype, int num_cus,
                           GemvPlan* p) {
-  if (variant != 1 && variant != 2) return false;
+  if (variant < 1 || variant > 3) return false;
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const uint32_t bpr = (in_dim + kQK - 1) / kQK;
-  const uint32_t block_bytes = variant == 1 ? RowsFmtXS::kBlockBytes : RowsFmtS::kBlockBytes;
+  const uint32_t block_bytes = variant_block_bytes(variant);
+  const uint32_t scale_bytes = variant_scale_bytes(variant);
   if (in_dim % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 ||
       (size_t)in_dim * esize % 16 != 0 || reinterpret_cast<uintptr_t>(ws) % 4 != 0 ||
       reinterpret_cast<uintptr_t>(wb) % (variant == 1 ? 16 : 8) != 0 || bpr % 4 != 0)
     return false;
-  if ((uint64_t)out_dim * bpr * RowsFmtXS::kScaleBytes > kOutOfRange - 4096) return false;
+  if ((uint64_t)out_dim * bpr * scale_bytes > kOutOfRange - 4096) return false;
   if ((uint64_t)out_dim * bpr * block_bytes > kOutOfRange - 4096) return false;
-  const uint32_t tables = variant == 1 ? RowsFmtXS::kTableBytes : RowsFmtS::kTableBytes;
-  if (!plan_gemv(1, out_dim, in_dim, x_dtype, num_cus, p, RowsFmtXS::kScaleBytes, 3, tables))
+  const uint32_t tables = variant == 1 ? RowsFmtXS::kTableBytes
+                                       : (variant == 2 ? RowsFmtS::kTableBytes
+                                                       : RowsFmtS3::kTableBytes);
+  if (!plan_gemv(1, out_dim, in_dim, x_dtype, num_cus, p, scale_bytes, variant == 3 ? 2 : 3,
+                 tables))
     return false;
   return p->wide && p->nchunks <= p->grid && p->ntasks <= kGemvThreads * p->xt;
 }
@@ -993,12 +1075,13 @@ hipError_t launch_iq_variant_gemv(int variant, const void* x, int x_dtype, const
   GemvPlan p;
   if (!plan_gemv_h16(variant, x, wb, ws, out_dim, in_dim, x_dtype, num_cus, &p))
     return hipErrorInvalidValue;
-  const GemvArgs a =
-      gemv_args(x, x_dtype, 1, wb, ws, out, out_dim, in_dim, w8a8, nullptr, p,
-                RowsFmtXS::kScaleBytes,
-                variant == 1 ? RowsFmtXS::kBlockBytes : RowsFmtS::kBlockBytes);
-  return variant == 1 ? launch_gemv_h16_f<kGemvXS>(a, p, x_dtype, w8a8, stream)
-                      : launch_gemv_h16_f<kGemvS>(a, p, x_dtype, w8a8, stream);
+  const GemvArgs a = gemv_args(x, x_dtype, 1, wb, ws, out, out_dim, in_dim, w8a8, nullptr, p,
+                               variant_scale_bytes(variant), variant_block_bytes(variant));
+  switch (variant) {
+    case 1: return launch_gemv_h16_f<kGemvXS>(a, p, x_dtype, w8a8, stream);
+    case 2: return launch_gemv_h16_f<kGemvS>(a, p, x_dtype, w8a8, stream);
+    default: return launch_gemv_h16_f<kGemvS3>(a, p, x_dtype, w8a8, stream);
+  }
 }
 
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,

@@ -90,7 +90,7 @@ hipError_t launch_iq_variant_matmul(int variant, const void* x, int x_dtype, uin
 // launches of up to 8 rows (W8A8: 32, int8 activations; row scales computed in
 // the kernel).  Needs
 // weight_bytes 16-byte and weight_scales 2-byte aligned.
-// IQ2_XS (variant 1) and IQ2_S (2) at m = 1 on the one-row GEMV
+// IQ2_XS (variant 1), IQ2_S (2) and IQ3_S (3) at m = 1 on the one-row GEMV
 // (iq2xxs_gemv.hip): whether the launch fits (alignment of x and the weight
 // buffers, K in whole 1024-column slices, one chunk per workgroup), and the
 // launch.

@@ -1,10 +1,10 @@
 """GPU parity of the IQ2_XS / IQ2_S / IQ3_S matmuls on the multi-row decode
 kernel (the one IQ2_XXS uses for 2..16 rows, with a format policy per variant),
-and of IQ2_XS and IQ2_S at m = 1 on the one-row GEMV.
+and of all three at m = 1 on the one-row GEMV.
 
 With weight_bytes 16-byte and weight_scales 2-byte aligned, every m runs
-there, in launches of up to 16 activation rows (IQ2_XS and IQ2_S at m = 1 with
-K in whole 1024-column slices: the one-row GEMV).  The reference computes each
+there, in launches of up to 16 activation rows (at m = 1 with K in whole
+1024-column slices: the one-row GEMV).  The reference computes each
 output on its own (iq2_matmul.metal:242-434, 501-699), so the bar is the
 IQ2_XXS GEMV's: against the fp64 oracle product of the same x (W8A8: of the
 fake-quantised x), cond <= 1e-5 and rel <= 1e-3 (definitions in
@@ -162,11 +162,11 @@ def test_variant_rows_nonfinite_x(pkg, oracle, dev, v, pattern):
     assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
 
 
-# ---------------------------- IQ2_XS and IQ2_S at m = 1: the one-row GEMV
+# ----------------- IQ2_XS, IQ2_S and IQ3_S at m = 1: the one-row GEMV
 # (K in whole 1024-column slices, 16-byte aligned x, weight_scales 4-byte and
-# weight_bytes 16-byte (IQ2_XS) / 8-byte (IQ2_S) aligned)
+# weight_bytes 16-byte (IQ2_XS) / 8-byte aligned)
 
-@pytest.mark.parametrize("v", [XS, S])
+@pytest.mark.parametrize("v", [XS, S, S3])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("out_dim,in_dim", [(14336, 4096), (4096, 14336), (777, 3072)])
 def test_one_row_vs_oracle(pkg, oracle, dev, v, dtype, out_dim, in_dim):
@@ -176,7 +176,7 @@ def test_one_row_vs_oracle(pkg, oracle, dev, v, dtype, out_dim, in_dim):
     _check(pkg, oracle, v, xt, wb, ws, out_dim, in_dim, dev)
 
 
-@pytest.mark.parametrize("v", [XS, S])
+@pytest.mark.parametrize("v", [XS, S, S3])
 def test_one_row_w8a8(pkg, oracle, dev, v):
     out_dim, in_dim = 2048, 4096
     wb, ws = random_weights(oracle, v, out_dim, in_dim, 181 + v)
@@ -184,7 +184,7 @@ def test_one_row_w8a8(pkg, oracle, dev, v):
     _check(pkg, oracle, v, xt, wb, ws, out_dim, in_dim, dev, w8a8=True)
 
 
-@pytest.mark.parametrize("v", [XS, S])
+@pytest.mark.parametrize("v", [XS, S, S3])
 @pytest.mark.parametrize("pattern", ["nan", "posinf", "both_inf", "inf_and_nan"])
 def test_one_row_nonfinite_x(pkg, oracle, dev, v, pattern):
     """A NaN or an infinity in x at m = 1: output classes exactly the
@@ -214,7 +214,7 @@ def test_one_row_nonfinite_x(pkg, oracle, dev, v, pattern):
         assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
 
 
-@pytest.mark.parametrize("v", [XS, S])
+@pytest.mark.parametrize("v", [XS, S, S3])
 def test_one_row_equals_its_own_row_in_a_pair(pkg, oracle, dev, v):
     """The one-row GEMV (m = 1) and the multi-row kernel (m = 2) on the same
     row agree to the GEMV bar (they sum in different orders)."""
