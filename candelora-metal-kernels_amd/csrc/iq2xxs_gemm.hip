@@ -729,14 +729,27 @@ size_t gemm_f32_scratch_bytes(uint32_t m, uint32_t in_dim, bool w8a8) {
   return (w8a8 ? 1 : 2) * (size_t)m * in_dim * 2;
 }
 
-// Sum of the k-split partials in split order (deterministic).
+// Sum of the k-split partials in split order (deterministic).  The loads of
+// up to kReduceBatch splits are issued before their adds, so a thread waits
+// for one memory round trip per batch rather than one per split; the adds
+// keep split order.
+constexpr uint32_t kReduceBatch = 16;
+
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ part,
                                                                 uint32_t splits, uint64_t n,
                                                                 float* __restrict__ out) {
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (uint64_t)gridDim.x * blockDim.x) {
     float v = part[i];
-    for (uint32_t z = 1; z < splits; ++z) v += part[z * n + i];
+    for (uint32_t zb = 1; zb < splits; zb += kReduceBatch) {
+      float w[kReduceBatch];
+#pragma unroll
+      for (uint32_t j = 0; j < kReduceBatch; ++j)
+        if (zb + j < splits) w[j] = part[(uint64_t)(zb + j) * n + i];
+#pragma unroll
+      for (uint32_t j = 0; j < kReduceBatch; ++j)
+        if (zb + j < splits) v += w[j];
+    }
     out[i] = v;
   }
 }
@@ -748,12 +761,20 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(const float4* _
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
        i += (uint64_t)gridDim.x * blockDim.x) {
     float4 v = part[i];
-    for (uint32_t z = 1; z < splits; ++z) {
-      const float4 w = part[z * n4 + i];
-      v.x += w.x;
-      v.y += w.y;
-      v.z += w.z;
-      v.w += w.w;
+    for (uint32_t zb = 1; zb < splits; zb += kReduceBatch) {
+      float4 w[kReduceBatch];
+#pragma unroll
+      for (uint32_t j = 0; j < kReduceBatch; ++j)
+        if (zb + j < splits) w[j] = part[(uint64_t)(zb + j) * n4 + i];
+#pragma unroll
+      for (uint32_t j = 0; j < kReduceBatch; ++j) {
+        if (zb + j < splits) {
+          v.x += w[j].x;
+          v.y += w[j].y;
+          v.z += w[j].z;
+          v.w += w[j].w;
+        }
+      }
     }
     out[i] = v;
   }
