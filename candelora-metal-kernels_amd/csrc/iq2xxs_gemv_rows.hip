@@ -56,6 +56,7 @@
 // Bound: HBM (the same algorithmic bytes as the one-row kernel; every weight
 // byte is read once, x once per workgroup from L2).
 #include <atomic>
+#include <type_traits>
 
 #include "iq2xxs_device.h"
 #include "iq2xxs_gemv_common.h"
@@ -78,11 +79,15 @@ constexpr uint32_t rows_tasks(uint32_t rows, bool w8a8, uint32_t m) {
 // Units of the first slice issued before the set-up work (tables, digits); the
 // rest are issued one per computed unit.  A CU's memory pipeline stalls a wave
 // at issue while it is full, so weight requests issued ahead of a barrier
-// would hold every wave at that barrier until they drain.  W8A8, whose set-up
-// (int8 rows, no digit planes) is shorter, takes two (0.4 us less at 4 and 8
-// rows; one more unit early did not help mode Off, and slowed IQ2_XS at M=1).
-template <bool kW8A8>
-constexpr uint32_t rows_units_early() { return kW8A8 ? 2 : 1; }
+// would hold every wave at that barrier until they drain.  Two units go
+// early (W8A8: 0.4 us less at 4 and 8 rows; mode Off, timed side by side:
+// IQ2_XXS 0.05-0.3 us less at 4 and 8 rows, IQ3_S 0.2-0.5 us less, IQ2_XS
+// level) except for IQ2_S in mode Off (three loads per unit), where two early
+// units were 0.5-0.9 us slower.
+template <class F, bool kW8A8>
+constexpr uint32_t rows_units_early() {
+  return (kW8A8 || !std::is_same<F, RowsFmtS>::value) ? 2 : 1;
+}
 // Flags and the W8A8 row scales.
 constexpr uint32_t rows_flag_bytes(uint32_t rows) { return (16 + 4 * rows + 15) & ~15u; }
 
@@ -132,7 +137,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
   constexpr uint32_t kAOps = (!kW8A8 && kRows == 16) ? 2 : 1;
   constexpr uint32_t kTO = kT / kAOps;  // activation-row pairs per A operand
   constexpr uint32_t kU = rows_units<F>(kRows, kVecX, kW8A8);
-  constexpr uint32_t kEarly = rows_units_early<kW8A8>();
+  constexpr uint32_t kEarly = rows_units_early<F, kW8A8>();
   // scale staging: 2-byte tasks per thread (a chunk holds R * 32 rows and a
   // slice S blocks, R * S <= 8 kU)
   constexpr uint32_t kSH = F::kScaleBytes / 2;
