@@ -197,11 +197,12 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   constexpr uint32_t kSL = kH16 ? 3 : kScaleLoads;
   constexpr uint32_t kLPT = kS ? 3 : (kS3 ? 4 : 1);  // load instructions per tile
   // Tiles in flight ahead of the one computed, and those of them issued
-  // before the set-up work.  IQ2_S and IQ3_S (three and four loads a tile) in
-  // mode Off keep one: timed side by side, IQ2_S read 9.3 against 11.0 us and
-  // IQ3_S 11.0 against 12.4 us with one instead of three (two: 10.5 and 11.5
-  // us); W8A8 was level.
-  constexpr uint32_t kTilesAhead = ((kS || kS3) && !kW8A8) ? 1 : 3;
+  // before the set-up work.  Mode Off keeps one (IQ2_XS three), timed side by
+  // side against three: IQ2_S 9.3 against 11.0 us, IQ3_S 11.0 against 12.4 us
+  // (three and four loads a tile); IQ2_XXS 6.99 against 7.13 us at K=4096
+  // N=14336, 7.80 against 8.00 us at K=14336 N=4096, 1-2 % slower at K=8192.
+  // W8A8 was level or slower with fewer.
+  constexpr uint32_t kTilesAhead = (!kXS && !kW8A8) ? 1 : 3;
   constexpr uint32_t kTilesFirst = kTilesEarly < kTilesAhead ? kTilesEarly : kTilesAhead;
   uint16_t* sscale = reinterpret_cast<uint16_t*>(lds + a.scale_ofs);
   float* xsc = reinterpret_cast<float*>(lds + a.xsc_ofs);
