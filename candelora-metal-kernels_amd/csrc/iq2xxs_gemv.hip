@@ -690,6 +690,14 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // Only runs for rows that held such a value.
   auto fix_up_special = [&](uint32_t mrow) {
     sync();  // the partial sums in red are consumed: red holds the kinds now
+    if (kW8A8 && inv_row == 0.0f) {
+      // an infinite activation makes the row's max infinite and inv 0: every
+      // q / inv is NaN, and so is every output, as in the reference (uniform;
+      // each thread writes the rows it wrote the sums of)
+      for (uint32_t rl = tid; rl < rows; rl += kGemvThreads)
+        a.out[(size_t)mrow * a.out_dim + row_begin + rl] = __builtin_nanf("");
+      return;
+    }
     for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) s_kinds[rl] = 0;
     sync();
     const size_t xbase = (size_t)mrow * a.in_dim;

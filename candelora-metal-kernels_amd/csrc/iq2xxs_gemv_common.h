@@ -1,5 +1,6 @@
 // iq2xxs_gemv_common.h — pieces shared by the decode-shaped IQ2_XXS kernels
-// (iq2xxs_gemv.hip: one activation row; iq2xxs_gemv_rows.hip: up to 8 rows):
+// (iq2xxs_gemv.hip: one activation row; iq2xxs_gemv_rows.hip: up to 16 rows,
+// W8A8 32):
 // the LDS expansion tables of the codebook and sign masks, LDS and buffer
 // access helpers, and the activation loads of a digitisation task.
 #pragma once

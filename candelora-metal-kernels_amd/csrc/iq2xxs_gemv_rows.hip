@@ -558,6 +558,16 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
       const uint32_t rows = min(R * 32, a.out_dim - min(chunk_row0, a.out_dim));
       for (uint32_t xrow = 0; xrow < a.m; ++xrow) {
         if (!((special >> xrow) & 1u)) continue;
+        if constexpr (kW8A8) {
+          // an infinite activation makes the row's max infinite and inv 0:
+          // every q / inv of the row is NaN, and so is every output, as in the
+          // reference (uniform branch)
+          if (s_inv[xrow] == 0.0f) {
+            for (uint32_t rl = tid; rl < rows; rl += kRowsThreads)
+              a.out[(size_t)xrow * a.out_dim + chunk_row0 + rl] = __builtin_nanf("");
+            continue;
+          }
+        }
         for (uint32_t rl = tid; rl < rows; rl += kRowsThreads) s_kinds[rl] = 0;
         sync();
         float inv = 1.0f;

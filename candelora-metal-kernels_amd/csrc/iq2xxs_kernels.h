@@ -16,7 +16,7 @@ hipError_t launch_iq2xxs_dequant(const uint8_t* wb, const uint8_t* ws, void* out
                                  hipStream_t stream);
 
 // Decode-shaped matmul (int8-MFMA GEMV), any m: the one-row kernel for m = 1,
-// the multi-row kernel on groups of up to 8 rows otherwise; shapes where
+// the multi-row kernel on groups of up to 16 rows (W8A8: 32) otherwise; shapes where
 // gemv_supported() holds (m = 1: K up to about 31000; weights and x below
 // 2 GB).  Needs 16-byte aligned weight_bytes and 2-byte aligned weight_scales.
 // gate non-null: out = silu(gate) * (x . w) with gate [m, out_dim] f32 (not
@@ -26,7 +26,7 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream,
                               const float* gate = nullptr);
-// The multi-row kernel alone (1 <= m <= 8; W8A8: 1 <= m <= 32).
+// The multi-row kernel alone (1 <= m <= 16; W8A8: 1 <= m <= 32).
 bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype,
                          bool w8a8 = false);
 hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
@@ -87,7 +87,7 @@ hipError_t launch_iq_variant_matmul(int variant, const void* x, int x_dtype, uin
                                     uint32_t out_dim, uint32_t in_dim, const float* row_inv,
                                     int num_cus, hipStream_t stream);
 // The multi-row decode kernel for IQ2_XS (1), IQ2_S (2), IQ3_S (3): any m, in
-// launches of up to 8 rows (W8A8: 32, int8 activations; row scales computed in
+// launches of up to 16 rows (W8A8: 32, int8 activations; row scales computed in
 // the kernel).  Needs
 // weight_bytes 16-byte and weight_scales 2-byte aligned.
 // IQ2_XS (variant 1), IQ2_S (2) and IQ3_S (3) at m = 1 on the one-row GEMV

@@ -34,7 +34,10 @@
 extern "C" {
 #endif
 
-#define CMK_IQ2_ABI_VERSION 1
+/* 2: cmk_iq2_matmul_noalloc and cmk_iq2_matmul_swiglu exported; f32 x at 9-16
+ * rows and W8A8 at 17-32 rows run on the multi-row decode kernel, with the
+ * workspace sizes that follow from it. */
+#define CMK_IQ2_ABI_VERSION 2
 
 /* Status codes. */
 typedef enum cmk_status {
@@ -49,10 +52,13 @@ typedef enum cmk_status {
  * reference accepts for x: F32, F16, BF16 (src/iq2_matmul.rs:59-75). */
 typedef enum cmk_dtype { CMK_F32 = 0, CMK_F16 = 1, CMK_BF16 = 2 } cmk_dtype;
 
-/* Iq2MatmulVariant (src/iq2_matmul.rs:31-37).  All four are implemented: IQ2_XXS
- * on the tuned GEMV / GEMM kernels, IQ2_XS / IQ2_S / IQ3_S on a portable wave-per-
- * row kernel (any m, any buffer alignment).  Bytes / scales per 256-weight block:
- * 64/2, 64/10, 72/10, 104/6 (src/iq2_matmul.rs:13-29). */
+/* Iq2MatmulVariant (src/iq2_matmul.rs:31-37).  All four are implemented.  IQ2_XXS
+ * runs on the one-row GEMV (m = 1), the multi-row decode kernel (up to 16 rows per
+ * launch, W8A8 32) and the MFMA GEMM (larger m).  IQ2_XS / IQ2_S / IQ3_S run on the
+ * one-row GEMV at m = 1 and on the multi-row decode kernel otherwise when the
+ * buffers are aligned (weight_bytes 16-byte or 8-byte, weight_scales 2-byte), and
+ * on a byte-load kernel for any other alignment.  Bytes / scales per 256-weight
+ * block: 64/2, 64/10, 72/10, 104/6 (src/iq2_matmul.rs:13-29). */
 typedef enum cmk_iq2_variant {
     CMK_IQ2_XXS = 0,
     CMK_IQ2_XS = 1,

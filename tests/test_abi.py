@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol(cabi):
     for s in syms:
         assert hasattr(L, s), s
     assert sorted(cabi.EXPORTED) == syms
-    assert L.cmk_abi_version() == 1
+    assert L.cmk_abi_version() == 2
 
 
 NULL = None

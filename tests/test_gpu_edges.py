@@ -112,6 +112,89 @@ def test_w8a8_nonfinite_x(pkg, oracle, inputs, dev, m):
         assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
 
 
+def _check_classes_and_finite(oracle, y, xf, wb, ws, out_dim, in_dim, w8a8=False):
+    """Output classes exactly the oracle's; finite outputs to the GEMV bar
+    against the fp64 product (non-finite activations set aside)."""
+    m = xf.shape[0]
+    if w8a8:
+        ref = oracle.matmul_reference_w8a8(xf, m, out_dim, in_dim, wb, ws)
+    else:
+        ref, _ = oracle.matmul_reference_mt(xf, m, out_dim, in_dim, wb, ws)
+    assert np.array_equal(classes(y), classes(ref))
+    fin = classes(ref) == 0
+    rows = [r for r in range(m) if fin[r].all()]
+    if rows:
+        xr = xf[rows]
+        if w8a8:
+            xr = oracle.rowwise_qdq_w8a8(xr, len(rows), in_dim)
+        y64, sc = oracle.matmul_f64(np.ascontiguousarray(xr), len(rows), out_dim, in_dim, wb, ws)
+        cond, rel = errors(y[rows], y64, sc)
+        assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
+    return ref
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [12, 16])
+def test_gemv_rows_nonfinite_high_rows(pkg, oracle, inputs, dev, dtype, m):
+    """The 16-row decode kernel keeps rows 8-15 in a second A operand with
+    their own flags: a NaN in row 9, +inf in row 11 and -inf in row m-1 reach
+    exactly those output rows, as in the reference's loop; rows 0-7 and the
+    other high rows stay finite."""
+    out_dim, in_dim = 1024, 4096
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim) == "gemv"
+    wb, ws = _weights_with_zero_d(inputs, out_dim, in_dim, [5, 600], 3)
+    x = inputs.synthetic_x(m, in_dim, seed=m)
+    x[9, 100] = np.nan
+    x[11, 2049] = np.inf
+    x[m - 1, 7] = -np.inf
+    xt = x_tensor(x, dtype, dev)
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    _check_classes_and_finite(oracle, y, x_as_f32(xt), wb, ws, out_dim, in_dim)
+    assert np.all(np.isnan(y[9]))
+    assert np.all(np.isfinite(y[:8]))
+
+
+def test_w8a8_rows_nonfinite_high_rows(pkg, oracle, inputs, dev):
+    """W8A8 with 20 rows on the 32-row int8 decode kernel: an infinity in row
+    17 (inv = 0: every output of the row is NaN) and a NaN in row 9; the other
+    rows to the GEMV bar against the reference's quantised activations."""
+    m, out_dim, in_dim = 20, 1024, 4096
+    cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim,
+                                pkg.cabi.CMK_ACT_QUANT_W8A8) == "gemv"
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    x = inputs.synthetic_x(m, in_dim, seed=20)
+    x[17, 5] = np.inf
+    x[9, 300] = np.nan
+    xt = x_tensor(x, torch.float32, dev)
+    y = pkg.iq2_matmul_with_activation_quant(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim,
+                                             in_dim, pkg.Iq2MatmulVariant.Iq2Xxs, cfg)
+    y = y.cpu().numpy()
+    _check_classes_and_finite(oracle, y, x_as_f32(xt), wb, ws, out_dim, in_dim, w8a8=True)
+    assert np.all(np.isnan(y[17])) and np.all(np.isnan(y[9]))
+
+
+def test_matmul_swiglu_nonfinite_high_rows(pkg, inputs, dev):
+    """silu(gate) * (x . w) with 13 rows: an infinity in row 10 of x (the
+    fix-up path of the high rows) and a NaN gate in row 12 give the bits of
+    the matmul followed by swiglu."""
+    m, k, n = 13, 4096, 1024
+    wu, su = inputs.synthetic_weights(n, k, seed=41)
+    wut, sut = to_dev(wu, dev), to_dev(su, dev)
+    x = torch.from_numpy(inputs.synthetic_x(m, k, seed=42)).to(dev)
+    x[10, 77] = float("inf")
+    gate = torch.from_numpy(inputs.synthetic_x(m, n, seed=43)).to(dev)
+    gate[12, 5] = float("nan")
+    ref = pkg.swiglu(gate, pkg.iq2_xxs_matmul(x, wut, sut, n, k))
+    got = pkg.iq2_matmul_swiglu(x, wut, sut, n, k, gate)
+    assert torch.equal(torch.isnan(ref), torch.isnan(got))
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(got))
+    assert torch.equal(ref[fin], got[fin])
+    assert not torch.isfinite(got[10]).all()
+
+
 @pytest.mark.parametrize("pattern", ["nan", "posinf", "both_inf"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_gemm_nonfinite_x(pkg, oracle, inputs, dev, pattern, dtype):

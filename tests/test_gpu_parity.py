@@ -173,7 +173,26 @@ GEMV_CASES = [
     (2, 1028, 28672),    # config 4 down-proj K
     (1, 28672, 8192),    # config 4 gate/up at M=1: four row chunks per workgroup
     (1, 8192, 28672),    # config 4 down at M=1: several chunks, digits in more than one round
+    (1, 8192, 8192),     # config 4 q/o at M=1
+    (1, 1024, 8192),     # config 4 k/v at M=1: one row group per workgroup, waves without a tile
 ]
+
+# BASELINE config 4 (Llama-3-70B layer) at M=1: every projection shape, with
+# f16 and bf16 activations as well as f32.
+CONFIG4_M1 = [(8192, 8192), (1024, 8192), (28672, 8192), (8192, 28672)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("out_dim,in_dim", CONFIG4_M1)
+def test_gemv_config4_m1_half_x(pkg, oracle, inputs, dev, dtype, out_dim, in_dim):
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim)
+    xt = x_tensor(inputs.synthetic_x(1, in_dim), dtype, dev)
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F16, 1, out_dim, in_dim) == "gemv"
+    y = pkg.iq2_matmul(xt, to_dev(wb, dev), to_dev(ws, dev), out_dim, in_dim,
+                       pkg.Iq2MatmulVariant.Iq2Xxs).cpu().numpy()
+    y64, sc = oracle.matmul_f64(x_as_f32(xt), 1, out_dim, in_dim, wb, ws)
+    cond, rel = errors(y, y64, sc)
+    assert cond <= 1e-5 and rel <= 1e-3, (out_dim, in_dim, cond, rel)
 
 
 @pytest.mark.parametrize("m,out_dim,in_dim", GEMV_CASES)

@@ -8,6 +8,10 @@ the W8A8 row scales and staged rows, and k-split partials).  Arguments that
 need more than the array holds are refused before anything is launched.
 """
 
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 
@@ -96,3 +100,95 @@ def test_noalloc_refuses_more_than_its_scratch(pkg, dev):
     with pytest.raises(cabi.CmkError, match="cmk_iq2_matmul_noalloc needs"):
         cabi.matmul_noalloc_raw(fake, cabi.CMK_F32, m * k, m, fake, n * bpr * 64, fake,
                                 n * bpr * 2, n, k, fake)
+
+
+def _graph_case(cabi, inputs, dev, m, n, k, seed):
+    wb, ws = inputs.synthetic_weights(n, k, seed=seed)
+    xt = torch.from_numpy(inputs.synthetic_x(m, k, seed=seed + 1)).to(dev)
+    wbt, wst = torch.from_numpy(wb).to(dev), torch.from_numpy(ws).to(dev)
+    args = (xt.data_ptr(), cabi.CMK_F32, xt.numel(), m, wbt.data_ptr(), wbt.numel(),
+            wst.data_ptr(), wst.numel(), n, k)
+    return (xt, wbt, wst), args
+
+
+def test_noalloc_graph_replays_match(pkg, inputs, dev):
+    """cmk_iq2_matmul_noalloc captured in a HIP graph (torch.cuda.graph) on a
+    shape whose launch uses the scratch array (f32 rows staged as f16 head /
+    tail pairs): four replays, each after an eager noalloc call of another
+    shape that overwrites the array, every replay bit-identical to
+    cmk_iq2_matmul with a workspace of its own."""
+    cabi = pkg.cabi
+    m, n, k = 64, 1024, 4096
+    keep, args = _graph_case(cabi, inputs, dev, m, n, k, seed=5)
+    keep2, args2 = _graph_case(cabi, inputs, dev, 48, 768, 2048, seed=9)
+    need = cabi.workspace_size(cabi.CMK_F32, m, n, k)
+    assert cabi.matmul_path(cabi.CMK_F32, m, n, k) == "gemm" and need > 0
+    work = torch.empty((need,), dtype=torch.uint8, device=dev)
+    ref = torch.empty((m, n), dtype=torch.float32, device=dev)
+    cabi.matmul_raw(*args, ref.data_ptr(), workspace_ptr=work.data_ptr(), workspace_bytes=need)
+    other = torch.empty((48, 768), dtype=torch.float32, device=dev)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        cabi.matmul_noalloc_raw(*args, out.data_ptr(), stream=s.cuda_stream)  # eager warm-up
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        cabi.matmul_noalloc_raw(*args, out.data_ptr(), stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.fill_(float("nan"))
+        cabi.matmul_noalloc_raw(*args2, other.data_ptr())  # overwrites the scratch array
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), rep
+    del keep, keep2
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+from tests.conftest import load_package
+pkg = load_package()
+cabi, inputs = pkg.cabi, pkg.inputs
+dev = torch.device("cuda:0")
+m, n, k = 64, 1024, 4096
+wb, ws = inputs.synthetic_weights(n, k, seed=5)
+xt = torch.from_numpy(inputs.synthetic_x(m, k, seed=6)).to(dev)
+wbt, wst = torch.from_numpy(wb).to(dev), torch.from_numpy(ws).to(dev)
+args = (xt.data_ptr(), cabi.CMK_F32, xt.numel(), m, wbt.data_ptr(), wbt.numel(),
+        wst.data_ptr(), wst.numel(), n, k)
+need = cabi.workspace_size(cabi.CMK_F32, m, n, k)
+work = torch.empty((need,), dtype=torch.uint8, device=dev)
+ref = torch.empty((m, n), dtype=torch.float32, device=dev)
+cabi.matmul_raw(*args, ref.data_ptr(), workspace_ptr=work.data_ptr(), workspace_bytes=need)
+out = torch.full((m, n), float("nan"), dtype=torch.float32, device=dev)
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):  # the first noalloc call of the process
+    cabi.matmul_noalloc_raw(*args, out.data_ptr(), stream=s.cuda_stream)
+torch.cuda.synchronize()
+for rep in range(3):
+    out.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), rep
+print("first call under capture: ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture(pkg, dev):
+    """In a fresh process, the first cmk_iq2_matmul_noalloc call (which looks
+    up the device's scratch address) happens inside stream capture; the graph
+    replays give cmk_iq2_matmul's bits (one child process, one GPU user)."""
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE, repo],
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-4000:])
+    assert "first call under capture: ok" in r.stdout
