@@ -210,3 +210,28 @@ def test_swiglu_argument_errors(cabi):
     assert cabi.last_error() == "swiglu null pointer argument"
     assert L.cmk_swiglu(NULL, NULL, 0, 0, NULL, NULL) == cabi.CMK_OK
 
+
+
+def test_rust_ffi_declarations_match_header():
+    """The Rust binding (not built here) declares only functions of the header,
+    each with the header's parameter count."""
+    import re
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    rs = open(os.path.join(repo, "candelora-metal-kernels_amd", "rust", "src", "hip",
+                           "ffi.rs")).read()
+    hdr = open(os.path.join(repo, "include", "cmk_iq2.h")).read()
+
+    def params(text, name, open_pat):
+        m = re.search(open_pat % re.escape(name), text)
+        assert m, name
+        depth, i = 1, m.end()
+        while depth:
+            depth += {"(": 1, ")": -1}.get(text[i], 0)
+            i += 1
+        body = text[m.end():i - 1].strip()
+        return 0 if body in ("", "void") else body.count(",") + 1
+
+    names = re.findall(r"pub fn (cmk_\w+)\(", rs)
+    assert len(names) >= 10
+    for n in names:
+        assert params(rs, n, r"pub fn %s\(") == params(hdr, n, r"\b%s\("), n
