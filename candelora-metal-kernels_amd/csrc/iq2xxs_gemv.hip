@@ -247,12 +247,25 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   };
   uint32_t chunk = blockIdx.x;
   uint32_t row_begin, n_rg, rows, t0, cnt;  // the current chunk's
+  // slice and row group of this wave's tiles t0 + k of the current chunk
+  // (uniform; one division per chunk, then a carry per tile)
+  uint32_t tslice[kTilesPerWave], trgl[kTilesPerWave];
   auto set_chunk = [&](const ChunkGeom& g) {
     row_begin = g.row_begin;
     n_rg = g.n_rg;
     rows = g.rows;
     t0 = g.t0;
     cnt = g.cnt;
+    uint32_t sl = t0 / n_rg, rg = t0 - sl * n_rg;
+#pragma unroll
+    for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+      tslice[k] = sl;
+      trgl[k] = rg;
+      if (++rg == n_rg) {
+        rg = 0;
+        ++sl;
+      }
+    }
   };
   // Lane (b, j) loads pair b of row j of the tile: byte offset
   // (first row of the tile's row group) * row_bytes + slice * 256 (uniform)
@@ -268,12 +281,10 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // and the sign bytes are the tile's x, y and z, w)
   uint32_t qhs[kS || kS3 ? kTilesPerWave : 1];
   u32x2 sgs[kS3 ? kTilesPerWave : 1];  // IQ3_S: the sign bytes of the lane's sub-blocks
-  auto load_tile_of = [&](const ChunkGeom& g, uint32_t k) -> u32x4 {
-    const uint32_t tau = g.t0 + k;
-    const uint32_t slice = tau / g.n_rg;
-    const uint32_t rgl = tau - slice * g.n_rg;
+  auto load_tile_at = [&](uint32_t slice, uint32_t rgl, uint32_t g_row_begin, bool present,
+                          uint32_t k) -> u32x4 {
     if constexpr (kS) {
-      const uint32_t base = k < g.cnt ? (g.row_begin + rgl * 4) * row_bytes +
+      const uint32_t base = present ? (g_row_begin + rgl * 4) * row_bytes +
                                             slice * (kSlicePairs / 4) * RowsFmtS::kBlockBytes
                                       : kOutOfRange;  // uniform
       const u32x2 qs = __builtin_amdgcn_raw_buffer_load_b64(rw, base + tile_lane_ofs, 0,
@@ -286,7 +297,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     }
     if constexpr (kS3) {
       // (blocks are 8-byte aligned only: the 16 grid bytes as two 8-byte loads)
-      const uint32_t base = k < g.cnt ? (g.row_begin + rgl * 4) * row_bytes +
+      const uint32_t base = present ? (g_row_begin + rgl * 4) * row_bytes +
                                             slice * (kSlicePairs / 4) * RowsFmtS3::kBlockBytes
                                       : kOutOfRange;  // uniform
       const uint32_t o = base + tile_lane_ofs;
@@ -296,13 +307,20 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       qhs[k] = __builtin_amdgcn_raw_buffer_load_b16(rw, o + 64 - 14 * (b & 3), 0, kStreamLoad);
       return u32x4{q0.x, q0.y, q1.x, q1.y};
     }
-    const uint32_t base = k < g.cnt
-                              ? (g.row_begin + rgl * 4) * row_bytes + slice * (kSlicePairs * 16)
+    const uint32_t base = present
+                              ? (g_row_begin + rgl * 4) * row_bytes + slice * (kSlicePairs * 16)
                               : kOutOfRange;  // uniform
     return __builtin_amdgcn_raw_buffer_load_b128(rw, base + tile_lane_ofs, 0, kStreamLoad);
   };
+  auto load_tile_of = [&](const ChunkGeom& g, uint32_t k) -> u32x4 {
+    const uint32_t tau = g.t0 + k;
+    const uint32_t slice = tau / g.n_rg;
+    const uint32_t rgl = tau - slice * g.n_rg;
+    return load_tile_at(slice, rgl, g.row_begin, k < g.cnt, k);
+  };
+  // (the current chunk's tile k: positions from tslice / trgl)
   auto load_tile = [&](uint32_t k) -> u32x4 {
-    return load_tile_of(ChunkGeom{row_begin, n_rg, rows, t0, cnt}, k);
+    return load_tile_at(tslice[k], trgl[k], row_begin, k < cnt, k);
   };
   // Super-block scales of the chunk, staged as rows of a.spr entries (blocks
   // padded to whole slices) with zeros for padding rows and blocks.
@@ -506,26 +524,26 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // Staged entry of (row j, pair b): (rgl * 4) * spr + slice * 4 (uniform)
   // plus j * spr + b / 4 (this lane's constant).
   const uint32_t scale_lane_ofs = j * a.spr + (b >> 2);
+  // (branch-free: the four reads are in flight together; an absent tile's
+  // entry index is clamped into the staged copy and its d replaced by 0)
   auto load_tile_scales = [&]() {
-    uint32_t slice = t0 / n_rg;
-    uint32_t rgl = t0 - slice * n_rg;
+    const uint32_t ent_max = a.rg_per_chunk * 4 * a.spr - 1;  // last staged entry
 #pragma unroll
     for (uint32_t k = 0; k < kTilesPerWave; ++k) {
-      const uint32_t base = rgl * 4 * a.spr + slice * (kSlicePairs / 4);  // uniform
+      const uint32_t base = trgl[k] * 4 * a.spr + tslice[k] * (kSlicePairs / 4);  // uniform
+      const uint32_t e = min(base + scale_lane_ofs, ent_max);
       if constexpr (kOther) {
         // block (row, blk) at byte kSB * (row * bpr + blk) of the staged copy
-        const uint32_t ent = a.scale_ofs + kSB * (base + scale_lane_ofs);
-        dsc[k] = k < cnt ? half_bits_to_float(lds_u16(ent)) : 0.0f;
+        const uint32_t ent = a.scale_ofs + kSB * e;
+        const float dv = half_bits_to_float(lds_u16(ent));
+        dsc[k] = k < cnt ? dv : 0.0f;
         // IQ2_XS / IQ2_S: the lane's two sub-scale bytes; IQ3_S: its byte (two
         // nibbles), from an aligned 2-byte read
         ssc[k] = kS3 ? lds_u16(ent + 2 + (b & 2)) >> (8 * (b & 1))
                      : lds_u16(ent + 2 + 2 * (b & 3));
       } else {
-        dsc[k] = k < cnt ? half_bits_to_float(sscale[base + scale_lane_ofs]) * 0x1p-27f : 0.0f;
-      }
-      if (++rgl == n_rg) {
-        rgl = 0;
-        ++slice;
+        const float dv = half_bits_to_float(sscale[e]) * 0x1p-27f;
+        dsc[k] = k < cnt ? dv : 0.0f;
       }
     }
   };
@@ -533,7 +551,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   asm volatile("" : "+v"(k27));
   // This lane's partial of tile k (before the sum over the 16 blocks).
   auto compute_tile = [&](uint32_t k) -> float {
-    const uint32_t slice = (t0 + k) / n_rg;
+    const uint32_t slice = tslice[k];
     if (slice != cur_slice) {  // uniform
       cur_slice = slice;
       // a pair past the row end reads the last pair's digits: its d is 0
@@ -728,22 +746,15 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       const uint32_t tk = lane >> 4;  // the tile this lane's row holds
       uint32_t ofs = 0;
 #pragma unroll
-      for (uint32_t k = 0; k < kTilesPerWave; ++k) {
-        const uint32_t tau = t0 + k;
-        const uint32_t slice = tau / n_rg;  // uniform
-        const uint32_t rgl = tau - slice * n_rg;
-        ofs = tk == k ? (rgl * a.nslices + slice) * 4 : ofs;
-      }
+      for (uint32_t k = 0; k < kTilesPerWave; ++k)
+        ofs = tk == k ? (trgl[k] * a.nslices + tslice[k]) * 4 : ofs;
       if ((lane & 12) == 0 && tk < cnt) red[ofs + j] = v;
     } else {
 #pragma unroll
       for (uint32_t k = 0; k < kTilesPerWave; ++k) {
         if (k >= cnt) break;  // uniform
-        const uint32_t tau = t0 + k;
-        const uint32_t slice = tau / n_rg;
-        const uint32_t rgl = tau - slice * n_rg;
         const float v = sum_over_blocks(acc[k]);
-        if (lane < 4) red[(rgl * a.nslices + slice) * 4 + j] = v;
+        if (lane < 4) red[(trgl[k] * a.nslices + tslice[k]) * 4 + j] = v;
       }
     }
     sync();
