@@ -48,6 +48,11 @@ MALL_BYTES = 256 << 20
 
 METRIC = "IQ2_XXS matmul GB/s (%HBM peak) at M=1; TFLOP/s (%MFMA peak) at M=512"
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_config1_traffic.json")
+# Sources of the one-row GEMV: the traffic file records their digest when its
+# counters are summarised, and the bench line reports the traffic figure only
+# while the digest still matches (a stale figure is reported as null).
+GEMV_SOURCES = ["csrc/iq2xxs_gemv.hip", "csrc/iq2xxs_gemv_common.h", "csrc/iq2xxs_device.h",
+                "csrc/iq2xxs_format.h", "csrc/iq2xxs_kernels.h", "csrc/iq_rows_formats.h"]
 
 DECODE_SHAPES = [("gate", 4096, 14336), ("up", 4096, 14336), ("down", 14336, 4096)]
 # Untimed decode steps replayed right before the timed replay (about 7 ms of
@@ -69,6 +74,111 @@ def load_package():
 
 def alg_bytes(m, k, n, xbytes=4):
     return n * math.ceil(k / 256) * 66 + m * k * xbytes + m * n * 4
+
+
+def gemv_source_digest():
+    """sha256 (first 16 hex digits) over the one-row GEMV's source files."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in GEMV_SOURCES:
+        h.update(rel.encode())
+        with open(os.path.join(PKG_DIR, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def _counter_rows(run_dir):
+    """(kernel name, counter name, value) per dispatch from a rocprofv3
+    `--pmc ... --output-format csv` output folder."""
+    import csv
+    import glob
+    files = sorted(glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"),
+                             recursive=True))
+    if not files:
+        raise SystemExit(f"bench.py: no *counter_collection.csv under {run_dir}")
+    rows = []
+    for path in files:
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                rows.append((r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"]),
+                             r.get("Dispatch_Id", "")))
+    return rows
+
+
+def traffic_summary(root, out_path):
+    """Summarise the four counter passes under `root` (copy_FETCH_SIZE,
+    gemv_FETCH_SIZE, copy_WRITE_SIZE, gemv_WRITE_SIZE) into `out_path`.
+
+    Each counter is calibrated by what it reads for the 256 MiB device copy of
+    `--copy-calibration` (read 256 MiB, write 256 MiB); the GEMV figure is the
+    mean KiB per dispatch over every one-row GEMV launch of the run."""
+    copy_bytes = 256 << 20
+    res = {}
+    names = set()
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        cal = sorted(v for k, c, v, _ in _counter_rows(os.path.join(root, "copy_" + counter))
+                     if c == counter and "copyBuffer" in k)
+        if not cal:
+            raise SystemExit(f"bench.py: no copyBuffer dispatch in copy_{counter}")
+        cal_kib = cal[len(cal) // 2]
+        factor = copy_bytes / (cal_kib * 1024.0)
+        per_shape = {}
+        for k, c, v, _ in _counter_rows(os.path.join(root, "gemv_" + counter)):
+            if c == counter and "iq2xxs_gemv_kernel" in k:
+                per_shape.setdefault(k, []).append(v)
+                names.add(k)
+        if not per_shape:
+            raise SystemExit(f"bench.py: no one-row GEMV dispatch in gemv_{counter}")
+        allv = [v for vs in per_shape.values() for v in vs]
+        res[counter] = {"factor": factor, "calibration_kib": cal_kib,
+                        "mean_kib": sum(allv) / len(allv), "dispatches": len(allv),
+                        "per_kernel_mean_kib": {k: sum(vs) / len(vs)
+                                                for k, vs in per_shape.items()}}
+    fetch = res["FETCH_SIZE"]["mean_kib"] * 1024 * res["FETCH_SIZE"]["factor"]
+    write = res["WRITE_SIZE"]["mean_kib"] * 1024 * res["WRITE_SIZE"]["factor"]
+    alg = sum(alg_bytes(1, k, n) for _, k, n in DECODE_SHAPES) / len(DECODE_SHAPES)
+    summary = {
+        "kernels": sorted(names),
+        "workload": "config 1 decode step: gate K=4096 N=14336, up K=4096 N=14336, "
+                    "down K=14336 N=4096 (M=1, fp32 x)",
+        "source_digest": gemv_source_digest(),
+        "hbm_bytes_per_launch": round(fetch + write),
+        "fetch_bytes_per_launch": round(fetch),
+        "write_bytes_per_launch": round(write),
+        "algorithmic_bytes_per_launch": round(alg),
+        "fetch_size_factor": round(res["FETCH_SIZE"]["factor"], 4),
+        "write_size_factor": round(res["WRITE_SIZE"]["factor"], 4),
+        "counters": res,
+        "note": "mean over gate/up/down launches of FETCH_SIZE and WRITE_SIZE (KiB per "
+                "dispatch) times the factor a 256 MiB device copy needs to read 256 MiB / "
+                "write 256 MiB",
+    }
+    with open(out_path, "w") as f:
+        json.dump(summary, f, indent=1)
+        f.write("\n")
+    print(json.dumps({k: summary[k] for k in ("hbm_bytes_per_launch", "fetch_bytes_per_launch",
+                                              "write_bytes_per_launch",
+                                              "algorithmic_bytes_per_launch",
+                                              "source_digest")}))
+
+
+def load_traffic():
+    """(bytes per launch or None, source note) from the committed traffic file;
+    None when the file was measured on other GEMV sources than these."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None, "no traffic file"
+    try:
+        t = json.load(open(TRAFFIC_FILE))
+    except (OSError, ValueError) as e:
+        return None, f"traffic file unreadable: {e}"
+    now = gemv_source_digest()
+    if t.get("source_digest") != now:
+        return None, (f"profiles/gemv_config1_traffic.json was measured on GEMV sources "
+                      f"{t.get('source_digest')}, not these ({now}): not reported")
+    return t.get("hbm_bytes_per_launch"), (
+        "profiles/gemv_config1_traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, "
+        f"copy-calibrated, measured on these GEMV sources ({now}); read from the file, not "
+        "measured in this run")
 
 
 def log(msg):
@@ -611,9 +721,16 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (for rocprof counter calibration)")
+    ap.add_argument("--traffic-summary", metavar="DIR",
+                    help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE passes under DIR "
+                         "into profiles/gemv_config1_traffic.json (no GPU needed)")
     ap.add_argument("--only", choices=["decode", "prefill", "read-floor", "variants", "configs"],
                     help="time one line only and print it (for profiling runs)")
     args = ap.parse_args()
+
+    if args.traffic_summary:
+        traffic_summary(args.traffic_summary, TRAFFIC_FILE)
+        return
 
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} requested, but this build measures one GPU only "
@@ -671,12 +788,7 @@ def main():
     torch.cuda.synchronize()
     value = dec["step_bytes"] * args.steps / (dec["ms"] / 1e3) / 1e9
     achieved = dec["per_launch_bytes"] / (dec["mean_launch_us"] * 1e-6) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        try:
-            traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+    traffic, traffic_source = load_traffic()
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -696,9 +808,7 @@ def main():
         "frac_of_hbm_peak": value / HBM_PEAK_GBS,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "traffic_source": ("profiles/gemv_config1_traffic.json: rocprofv3 FETCH_SIZE "
-                                        "+ WRITE_SIZE per gate launch, copy-calibrated; read "
-                                        "from the file, not measured in this run"),
+                     "traffic_source": traffic_source,
                      "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false, 0> "
                                "(XT = 1 for K=4096, 2 for K=14336)",
                      "mean_launch_us": dec["mean_launch_us"],
