@@ -559,7 +559,8 @@ def bench_mlp_step(pkg, torch, stream, steps, k=4096, n=14336):
         gate()
         uw, us = sets[1][i % copies]
         cabi.matmul_swiglu_raw(x.data_ptr(), cabi.CMK_F32, k, 1, uw.data_ptr(), uw.numel(),
-                               us.data_ptr(), us.numel(), n, k, g.data_ptr(), n, h.data_ptr(), sh)
+                               us.data_ptr(), us.numel(), n, k, g.data_ptr(), n, h.data_ptr(),
+                               stream=sh)
         down()
 
     def timed(run):

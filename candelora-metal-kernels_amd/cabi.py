@@ -87,7 +87,7 @@ def lib() -> ctypes.CDLL:
     L.cmk_iq2_split_gguf_blocks.restype = I
     L.cmk_swiglu.argtypes = [P, P, S, I, P, P]
     L.cmk_swiglu.restype = I
-    L.cmk_iq2_matmul_swiglu.argtypes = [P, I, S, S, P, S, P, S, S, S, P, S, P, P]
+    L.cmk_iq2_matmul_swiglu.argtypes = [P, I, S, S, P, S, P, S, S, S, P, S, P, P, S, P]
     L.cmk_iq2_matmul_swiglu.restype = I
     L.cmk_iq2_dequantize.restype = I
     L.cmk_last_error.argtypes = []
@@ -164,9 +164,11 @@ def swiglu_raw(gate_ptr, up_ptr, n, out_ptr, out_dtype=CMK_F32, stream=None) -> 
 
 
 def matmul_swiglu_raw(x_ptr, x_dtype, x_len, m, wb_ptr, wb_len, ws_ptr, ws_len, out_dim, in_dim,
-                      gate_ptr, gate_len, out_ptr, stream=None) -> None:
+                      gate_ptr, gate_len, out_ptr, workspace_ptr=None, workspace_bytes=0,
+                      stream=None) -> None:
     check(lib().cmk_iq2_matmul_swiglu(x_ptr, x_dtype, x_len, m, wb_ptr, wb_len, ws_ptr, ws_len,
-                                      out_dim, in_dim, gate_ptr, gate_len, out_ptr, stream))
+                                      out_dim, in_dim, gate_ptr, gate_len, out_ptr, workspace_ptr,
+                                      workspace_bytes, stream))
 
 
 def dequantize_raw(wb_ptr, wb_len, ws_ptr, ws_len, out_dim, in_dim, out_ptr,

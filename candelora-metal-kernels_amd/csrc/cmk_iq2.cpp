@@ -127,13 +127,37 @@ size_t workspace_head(Path p, bool w8a8, int x_dtype, size_t m, uint32_t in_dim)
   return row_scale_bytes(m);
 }
 
-// The head, then for a GEMM split over k its partial products.
-size_t workspace_for(Path p, bool w8a8, int x_dtype, size_t m, uint32_t out_dim,
-                     uint32_t in_dim) {
+// What a launch needs: the head, then for a GEMM split over k its partial
+// products.
+size_t workspace_required(Path p, bool w8a8, int x_dtype, size_t m, uint32_t out_dim,
+                          uint32_t in_dim) {
   const size_t head = workspace_head(p, w8a8, x_dtype, m, in_dim);
   if (p != Path::Gemm) return head;
   const size_t rows = x_dtype == CMK_F32 && !w8a8 ? 2 * m : m;
   return head + cmk::gemm_split_scratch_bytes((uint32_t)rows, (uint32_t)m, out_dim, in_dim);
+}
+
+// The multi-row decode kernel splits K over several workgroups per row group
+// when the row groups leave CUs idle (N <= 4096 on 256 CUs); the split is
+// used when the workspace holds its bytes after the required ones (256-byte
+// aligned) and skipped otherwise.  The query assumes 256 CUs, the most a
+// gfx950 device has: fewer CUs never split more.
+constexpr int kMaxCusForQuery = 256;
+size_t split_offset(size_t required) {
+  return (required + kWorkspaceAlign - 1) / kWorkspaceAlign * kWorkspaceAlign;
+}
+size_t rows_split_bytes(Path p, bool w8a8, size_t m, uint32_t out_dim, uint32_t in_dim,
+                        int cus) {
+  if ((p != Path::Gemv && p != Path::Variant) || m < 2 || m > UINT32_MAX) return 0;
+  return cmk::gemv_rows_split_bytes((uint32_t)m, out_dim, in_dim, w8a8, cus);
+}
+
+// The workspace the query reports: the required bytes, then the split's.
+size_t workspace_for(Path p, bool w8a8, int x_dtype, size_t m, uint32_t out_dim,
+                     uint32_t in_dim) {
+  const size_t req = workspace_required(p, w8a8, x_dtype, m, out_dim, in_dim);
+  const size_t split = rows_split_bytes(p, w8a8, m, out_dim, in_dim, kMaxCusForQuery);
+  return split ? split_offset(req) + split : req;
 }
 
 // Shared validation of cmk_iq2_matmul / cmk_iq2_matmul_workspace_size.
@@ -298,7 +322,8 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   Path p = variant != CMK_IQ2_XXS ? Path::Variant
                                   : choose_path((int)x_dtype, m, dims.out_dim, dims.in_dim, x,
                                                 weight_bytes, weight_scales, w8a8);
-  const size_t need_ws = workspace_for(p, w8a8, (int)x_dtype, m, dims.out_dim, dims.in_dim);
+  const size_t need_ws =
+      workspace_required(p, w8a8, (int)x_dtype, m, dims.out_dim, dims.in_dim);
   const size_t head_ws = workspace_head(p, w8a8, (int)x_dtype, m, dims.in_dim);
   if (need_ws > 0 && (workspace == nullptr || workspace_bytes < need_ws))
     return fail(CMK_ERR_INVALID_ARGUMENT,
@@ -312,6 +337,15 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   int cus = 0;
   rc = current_cu_count(&cus);
   if (rc != CMK_OK) return rc;
+  // the multi-row kernel's split over K, when the workspace has room for it
+  void* split_ws = nullptr;
+  size_t split_ws_bytes = 0;
+  const size_t split_need = rows_split_bytes(p, w8a8, m, dims.out_dim, dims.in_dim, cus);
+  if (split_need > 0 && workspace != nullptr && aligned(workspace, 16) &&
+      workspace_bytes >= split_offset(need_ws) + split_need) {
+    split_ws = static_cast<uint8_t*>(workspace) + split_offset(need_ws);
+    split_ws_bytes = workspace_bytes - split_offset(need_ws);
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = hipSuccess;
   float* row_inv = head_ws > 0 ? static_cast<float*>(workspace) : nullptr;
@@ -335,7 +369,8 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
   switch (p) {
     case Path::Gemv:
       e = cmk::launch_iq2xxs_gemv(x, (int)x_dtype, dims.m, weight_bytes, weight_scales, out,
-                                  dims.out_dim, dims.in_dim, w8a8, cus, s);
+                                  dims.out_dim, dims.in_dim, w8a8, cus, s, nullptr, split_ws,
+                                  split_ws_bytes);
       break;
     case Path::Gemm:
       e = cmk::launch_iq2xxs_gemm(
@@ -355,7 +390,7 @@ int cmk_iq2_matmul(const void* x, cmk_dtype x_dtype, size_t x_len, size_t m,
           : variant_rows
               ? cmk::launch_iq_variant_rows((int)variant, x, (int)x_dtype, dims.m, weight_bytes,
                                             weight_scales, out, dims.out_dim, dims.in_dim, w8a8,
-                                            cus, s)
+                                            cus, s, split_ws, split_ws_bytes)
               : cmk::launch_iq_variant_matmul((int)variant, x, (int)x_dtype, dims.m,
                                               weight_bytes, weight_scales, out, dims.out_dim,
                                               dims.in_dim, row_inv, cus, s);
@@ -507,7 +542,7 @@ int cmk_iq2_matmul_swiglu(const void* x, cmk_dtype x_dtype, size_t x_len, size_t
                           const uint8_t* weight_bytes, size_t weight_bytes_len,
                           const uint8_t* weight_scales, size_t weight_scales_len,
                           size_t out_dim, size_t in_dim, const float* gate, size_t gate_len,
-                          float* out, void* stream) {
+                          float* out, void* workspace, size_t workspace_bytes, void* stream) {
   int md = CMK_ACT_QUANT_OFF;
   Dims dims;
   int rc = validate_matmul((int)x_dtype, m, out_dim, in_dim, CMK_IQ2_XXS, &md, 0,
@@ -542,9 +577,15 @@ int cmk_iq2_matmul_swiglu(const void* x, cmk_dtype x_dtype, size_t x_len, size_t
   int cus = 0;
   rc = current_cu_count(&cus);
   if (rc != CMK_OK) return rc;
-  const hipError_t e = cmk::launch_iq2xxs_gemv(x, (int)x_dtype, dims.m, weight_bytes,
-                                               weight_scales, out, dims.out_dim, dims.in_dim,
-                                               false, cus, static_cast<hipStream_t>(stream), gate);
+  // the split over K as cmk_iq2_matmul takes it (the GEMV path needs no other
+  // workspace)
+  const size_t split_need = rows_split_bytes(Path::Gemv, false, m, dims.out_dim, dims.in_dim, cus);
+  const bool split = split_need > 0 && workspace != nullptr && aligned(workspace, 16) &&
+                     workspace_bytes >= split_need;
+  const hipError_t e = cmk::launch_iq2xxs_gemv(
+      x, (int)x_dtype, dims.m, weight_bytes, weight_scales, out, dims.out_dim, dims.in_dim, false,
+      cus, static_cast<hipStream_t>(stream), gate, split ? workspace : nullptr,
+      split ? workspace_bytes : 0);
   if (e != hipSuccess) return hip_fail(e, "matmul_swiglu launch");
   return ok();
 }

@@ -1,17 +1,19 @@
-// iq2xxs_gemm.hip — prefill-shaped IQ2_XXS matmul (large m, x in f16/bf16).
+// iq2xxs_gemm.hip — prefill-shaped IQ2_XXS matmul (large m).
 //
-// out[m, n] = sum_k x[m, k] * W[n, k], W dequantised per tile into LDS in the
-// activation's type, then fed to v_mfma_f32_16x16x32_{f16,bf16} with fp32
-// accumulation.  Every dequantised value is the single round-to-nearest-even
-// of the exact weight d*(2s+1)*g/8, i.e. exactly what iq2_dequantize_to_f16
-// produces.
+// out[m, n] = sum_k x[m, k] * W[n, k], W dequantised per tile into LDS as
+// f16, then fed to v_mfma_f32_16x16x32_f16 with fp32 accumulation.  Every
+// dequantised value is the single round-to-nearest-even of the exact weight
+// d*(2s+1)*g/8, i.e. exactly what iq2_dequantize_to_f16 produces.  The
+// activations reach the kernel as f16: f16 x as given; bf16 x staged as f16
+// after scaling each row by a power of two (exact); f32 x staged as f16 head /
+// tail row pairs (about 22 bits of each value); W8A8 rows as their integer q.
 //
 // The reference has no dedicated prefill kernel: its iq2_xxs_matmul_kernel
 // (src/metal_src/iq2_matmul.metal:188-240) serves every m with one thread per
 // output.  This kernel is the large-m replacement on the same boundary.
 //
 // W8A8 (iq2_matmul.metal:436-499): a pre-pass writes q = clamp(round(x*inv),
-// +-127) (exact small integers in f16/bf16) to the caller's workspace; the
+// +-127) (exact small integers in f16) to the caller's workspace; the
 // GEMM runs on q and divides each fp32 result by its row's inv, i.e.
 // sum(q/inv * w) up to fp32 rounding.
 //
@@ -62,7 +64,6 @@
 namespace cmk {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -94,28 +95,16 @@ struct GemmLayout {
   static_assert(kTotal <= kGemmLdsLimit, "LDS budget");
 };
 
-template <bool kBf16>
 __device__ __forceinline__ float4v mfma16(const u32x4& a, const u32x4& b, float4v c) {
-  if constexpr (kBf16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
-                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
+                                                __builtin_bit_cast(half8, b), c, 0, 0, 0);
 }
 
-// Two floats as a packed pair of f16 / bf16 (each one round-to-nearest-even).
-template <bool kBf16>
+// Two floats as a packed pair of f16 (each one round-to-nearest-even).
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  if constexpr (kBf16) {
-    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    const b2 v = {(__bf16)lo, (__bf16)hi};
-    return __builtin_bit_cast(uint32_t, v);
-  } else {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 v = {(_Float16)lo, (_Float16)hi};
-    return __builtin_bit_cast(uint32_t, v);
-  }
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 v = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ __forceinline__ u32x4 gemm_lds_u4(uint32_t addr) {
@@ -133,7 +122,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p, uint3
 }
 
 struct GemmArgs {
-  const uint16_t* x;  // f16 or bf16 bits, [m, in_dim] (q for W8A8)
+  const uint16_t* x;  // f16 bits, [m, in_dim] (staged rows, or q for W8A8)
   const uint8_t* wb;
   const uint8_t* ws;
   float* out;
@@ -199,7 +188,7 @@ __device__ __forceinline__ void build_gemm_tables(uint32_t tid) {
 // kQ: 0 = plain output; 1 = output row r divided by row_inv[r]; 2 = staged
 // row pairs (2r: the f16 head of x_r * row_inv[r], 2r + 1: the f16 of what
 // the head leaves), output row r = (C[2r] + C[2r+1]) / row_inv[r].
-template <bool kBf16, int BM, int BN, int kQ>
+template <int BM, int BN, int kQ>
 __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
   using L = GemmLayout<BM, BN>;
   extern __shared__ __align__(16) uint8_t lds[];
@@ -277,8 +266,8 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     auto write_w = [&](uint32_t t, uint32_t aux_s, uint32_t dbits, const Tables& T) {
       // exact fp32 level values l * d * (2s + 1) / 8, then one rounding each
       const float tdf = half_bits_to_float((uint16_t)dbits) * (float)((aux_s >> 27) | 1u) * 0.125f;
-      const uint32_t pool_lo = pack2<kBf16>(8.0f * tdf, 25.0f * tdf);
-      const uint32_t pool_hi = pack2<kBf16>(43.0f * tdf, 0.0f);
+      const uint32_t pool_lo = pack2(8.0f * tdf, 25.0f * tdf);
+      const uint32_t pool_hi = pack2(43.0f * tdf, 0.0f);
 #pragma unroll
       for (int gg = 0; gg < 2; ++gg) {
         const u32x4 v = {__builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].x) ^ T.sgn[gg].x,
@@ -418,7 +407,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = i0; i < i0 + 2; ++i)
 #pragma unroll
-      for (int jn = 0; jn < NT; ++jn) acc[i][jn] = mfma16<kBf16>(F.a[i], F.b[jn], acc[i][jn]);
+      for (int jn = 0; jn < NT; ++jn) acc[i][jn] = mfma16(F.a[i], F.b[jn], acc[i][jn]);
   };
   // Rows 2-3 of stage F with the fragment reads of the next stage (into Fn)
   // interleaved one per MFMA, so that the MFMA pipe restarts right after a
@@ -435,7 +424,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
           Fn.a[k] = gemm_lds_u4(abase + k * 16 * 64);
         else if (k < 4 + NT)
           Fn.b[k - 4] = gemm_lds_u4(bbase + (k - 4) * 16 * 64);
-        acc[i][jn] = mfma16<kBf16>(F.a[i], F.b[jn], acc[i][jn]);
+        acc[i][jn] = mfma16(F.a[i], F.b[jn], acc[i][jn]);
         __builtin_amdgcn_sched_barrier(0);
         ++k;
       }
@@ -448,7 +437,7 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int jn = 0; jn < NT; ++jn) {
-        acc[i][jn] = mfma16<kBf16>(F.a[i], F.b[jn], acc[i][jn]);
+        acc[i][jn] = mfma16(F.a[i], F.b[jn], acc[i][jn]);
         __builtin_amdgcn_sched_barrier(0);
       }
   };
@@ -532,7 +521,7 @@ __global__ __launch_bounds__(256) void iq2xxs_quantize_rows_kernel(const uint16_
                              : half_bits_to_float((uint16_t)(w[k] >> 16));
       const float ql = quant_w8a8(lo, inv);
       const float qh = quant_w8a8(hi, inv);
-      o[k] = pack2<false>(ql, qh);
+      o[k] = pack2(ql, qh);
     }
     *reinterpret_cast<u32x4*>(q + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
   }
@@ -578,8 +567,8 @@ __global__ __launch_bounds__(256) void iq2xxs_scale_stage_bf16_rows_kernel(
     uint32_t o[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      o[k] = pack2<false>(bf16_bits_to_float((uint16_t)w[k]) * inv,
-                          bf16_bits_to_float((uint16_t)(w[k] >> 16)) * inv);
+      o[k] = pack2(bf16_bits_to_float((uint16_t)w[k]) * inv,
+                   bf16_bits_to_float((uint16_t)(w[k] >> 16)) * inv);
     o8[c] = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
@@ -601,7 +590,7 @@ __global__ __launch_bounds__(256) void iq2xxs_stage_f32_w8a8_kernel(const float*
     uint32_t o[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      o[k] = pack2<false>(quant_w8a8(v[2 * k], inv), quant_w8a8(v[2 * k + 1], inv));
+      o[k] = pack2(quant_w8a8(v[2 * k], inv), quant_w8a8(v[2 * k + 1], inv));
     *reinterpret_cast<u32x4*>(q + c * 8) = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
@@ -653,9 +642,9 @@ __global__ __launch_bounds__(256) void iq2xxs_scale_stage_f32_rows_kernel(
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const float h0 = (float)(_Float16)v[2 * k], h1 = (float)(_Float16)v[2 * k + 1];
-      oh[k] = pack2<false>(h0, h1);
-      ot[k] = pack2<false>(fin(v[2 * k]) ? v[2 * k] - h0 : 0.0f,
-                           fin(v[2 * k + 1]) ? v[2 * k + 1] - h1 : 0.0f);
+      oh[k] = pack2(h0, h1);
+      ot[k] = pack2(fin(v[2 * k]) ? v[2 * k] - h0 : 0.0f,
+                    fin(v[2 * k + 1]) ? v[2 * k + 1] - h1 : 0.0f);
     }
     *reinterpret_cast<u32x4*>(head + c * 8) = u32x4{oh[0], oh[1], oh[2], oh[3]};
     *reinterpret_cast<u32x4*>(head + in_dim + c * 8) = u32x4{ot[0], ot[1], ot[2], ot[3]};
@@ -706,9 +695,9 @@ __global__ __launch_bounds__(1024) void iq2xxs_stage_f32_rows_held_kernel(
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const float h0 = (float)(_Float16)e[2 * k], h1 = (float)(_Float16)e[2 * k + 1];
-      oh[k] = pack2<false>(h0, h1);
-      ot[k] = pack2<false>(fin(e[2 * k]) ? e[2 * k] - h0 : 0.0f,
-                           fin(e[2 * k + 1]) ? e[2 * k + 1] - h1 : 0.0f);
+      oh[k] = pack2(h0, h1);
+      ot[k] = pack2(fin(e[2 * k]) ? e[2 * k] - h0 : 0.0f,
+                    fin(e[2 * k + 1]) ? e[2 * k + 1] - h1 : 0.0f);
     }
     *reinterpret_cast<uint2*>(head + c * 4) = make_uint2(oh[0], oh[1]);
     *reinterpret_cast<uint2*>(head + in_dim + c * 4) = make_uint2(ot[0], ot[1]);
@@ -809,19 +798,19 @@ size_t gemm_split_scratch_bytes(uint32_t rows, uint32_t out_rows, uint32_t out_d
   return p.splits > 1 ? (size_t)p.splits * out_rows * out_dim * sizeof(float) : 0;
 }
 
-template <bool kBf16, int BM, int BN, int kQ>
+template <int BM, int BN, int kQ>
 static hipError_t launch_gemm_t(const GemmArgs& a, uint32_t splits, hipStream_t stream) {
   using L = GemmLayout<BM, BN>;
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&iq2xxs_gemm_kernel<kBf16, BM, BN, kQ>),
+        reinterpret_cast<const void*>(&iq2xxs_gemm_kernel<BM, BN, kQ>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLdsLimit);
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
   dim3 grid((a.out_dim + BN - 1) / BN, (a.m + BM - 1) / BM, splits);
-  hipLaunchKernelGGL((iq2xxs_gemm_kernel<kBf16, BM, BN, kQ>), grid, dim3(kGemmThreads),
+  hipLaunchKernelGGL((iq2xxs_gemm_kernel<BM, BN, kQ>), grid, dim3(kGemmThreads),
                      L::kTotal, stream, a);
   return hipGetLastError();
 }
@@ -829,7 +818,7 @@ static hipError_t launch_gemm_t(const GemmArgs& a, uint32_t splits, hipStream_t 
 // out_rows: rows of the output (a.m / 2 for staged pairs).  With a k split
 // the workgroups write partials (the caller's buffer of
 // gemm_split_scratch_bytes) that a second kernel sums into out.
-template <bool kBf16, int kQ>
+template <int kQ>
 static hipError_t launch_gemm_shape(GemmArgs a, uint32_t out_rows, float* partials,
                                     hipStream_t stream) {
   const GemmPlan p = plan_gemm(a.m, a.out_dim, a.in_dim);
@@ -843,8 +832,8 @@ static hipError_t launch_gemm_shape(GemmArgs a, uint32_t out_rows, float* partia
     a.out = partials;
     a.out_split = n;
   }
-  const hipError_t e = p.wide ? launch_gemm_t<kBf16, 256, 112, kQ>(a, p.splits, stream)
-                              : launch_gemm_t<kBf16, 128, 128, kQ>(a, p.splits, stream);
+  const hipError_t e = p.wide ? launch_gemm_t<256, 112, kQ>(a, p.splits, stream)
+                              : launch_gemm_t<128, 128, kQ>(a, p.splits, stream);
   if (e != hipSuccess || p.splits == 1) return e;
   if (n % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
       reinterpret_cast<uintptr_t>(partials) % 16 == 0) {
@@ -946,9 +935,9 @@ hipError_t launch_iq2xxs_gemm(const void* x, int x_dtype, uint32_t m, const uint
   a.out_split = 0;
   // every row set runs on f16 weights: f16 x as given, bf16 and f32 rows and
   // W8A8's q staged as f16 (row_inv: the scale the epilogue divides by)
-  if (x_dtype == 0 && !w8a8) return launch_gemm_shape<false, 2>(a, out_rows, partials, stream);
-  if (row_inv) return launch_gemm_shape<false, 1>(a, out_rows, partials, stream);
-  return launch_gemm_shape<false, 0>(a, out_rows, partials, stream);
+  if (x_dtype == 0 && !w8a8) return launch_gemm_shape<2>(a, out_rows, partials, stream);
+  if (row_inv) return launch_gemm_shape<1>(a, out_rows, partials, stream);
+  return launch_gemm_shape<0>(a, out_rows, partials, stream);
 }
 
 }  // namespace cmk

@@ -1111,7 +1111,8 @@ hipError_t launch_iq_variant_gemv(int variant, const void* x, int x_dtype, const
 
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
-                              bool w8a8, int num_cus, hipStream_t stream, const float* gate) {
+                              bool w8a8, int num_cus, hipStream_t stream, const float* gate,
+                              void* split_ws, size_t split_ws_bytes) {
   if (m > 1) {
     // groups of up to 16 activation rows (W8A8: 32), each decoding the weights once
     const size_t esize = x_dtype == 0 ? 4 : 2;
@@ -1120,7 +1121,8 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
       const hipError_t e = launch_iq2xxs_gemv_rows(
           static_cast<const uint8_t*>(x) + (size_t)r0 * in_dim * esize, x_dtype,
           m - r0 < group ? m - r0 : group, wb, ws, out + (size_t)r0 * out_dim, out_dim, in_dim,
-          w8a8, num_cus, stream, gate ? gate + (size_t)r0 * out_dim : nullptr);
+          w8a8, num_cus, stream, gate ? gate + (size_t)r0 * out_dim : nullptr, split_ws,
+          split_ws_bytes);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -14,10 +14,10 @@
 // v_mfma_i32_32x32x32_i8, with lane l supplying columns 8 (l/32) .. + 7 of
 // each 16-column half.
 //
-// Arithmetic.  The activations become the same exact integer digits as in the
-// one-row kernel (iq2xxs_gemv.hip): per 32-column sub-block, three signed 8-bit
-// planes of rint(x * 2^(D-e)), in LDS (D = 20 bits for IQ2_XXS, 21 for the
-// formats whose plane sums leave room for it).  The codes expand through the same
+// Arithmetic.  The activations become exact integer digits as in the one-row
+// kernel (iq2xxs_gemv.hip): per 32-column sub-block, three signed 8-bit planes
+// of rint(x * 2^(D-e)), in LDS, with D = 21 bits for every format (the one-row
+// kernel keeps 20 for IQ2_XXS).  The codes expand through the same
 // LDS tables ({g, -g} codebook rows, 8-byte sign masks, one bit select per
 // dword).  v_mfma_i32_32x32x32_i8 then takes
 //   A: 32 rows = 8 activation rows x 4 digit planes (plane 3 and absent rows
@@ -28,8 +28,10 @@
 // 16*(l/32) .. +15 of the sub-block (so A and B agree on the k order whatever
 // the hardware's byte order is), and receives C rows 8*(r/4) + 4*(l/32) + r%4
 // in register r: planes 0..2 of activation rows 2t + l/32 (t = r/4) against
-// weight row l%32.  The three plane sums combine exactly in int32; the scale
-// (2s+1) * 2^(e-D-3) is applied in fp32 per sub-block, d once per super-block.
+// weight row l%32.  The three plane sums combine exactly in int32 where they
+// fit (IQ2_XXS: 256 C2 + C1 exactly, then one fp32 rounding for the last
+// byte); the scale (2s+1) * 2^(e-D-3) is applied in fp32 per sub-block, d
+// once per super-block.
 //
 // Work split.  A *unit* is 32 weight rows x half a super-block (4 sub-blocks,
 // 1 KB of codes: one 16-byte load per lane).  A workgroup of 16 waves owns a
@@ -42,6 +44,19 @@
 // units read them: a unit's own scale bytes are a few scattered bytes per row,
 // which cost more than the unit's codes.  The waves of a row group add their
 // partial sums in wave order, so results are deterministic.
+//
+// Split over K.  When the row groups alone would leave CUs idle (fewer 32-row
+// groups than CUs: N = 4096 has 128), each row group's K range is cut into
+// `kparts` parts of whole slices, one workgroup each.  A part writes its sums
+// to the caller's workspace with agent-scope atomic stores, waits for them to
+// complete, then counts itself in on its row group's arrival word (an
+// agent-scope compare-and-swap); the part that arrives last reads every
+// part's sums with agent-scope atomic loads, adds them in part order -- the
+// same result whichever part is last -- and writes the outputs, the gated
+// step and the non-finite fix-up.  The word needs no initial value: it holds
+// (launch epoch, count), a count under another epoch counts as zero, and the
+// last part clears it, so replays of a captured launch (same epoch) start from
+// zero.  No workgroup waits for another.
 //
 // W8A8 (true int8).  The reference fake-quantises x per row (q / inv with q =
 // clamp(round(x * inv), +-127), iq2_matmul.metal:85-126) and multiplies in
@@ -109,7 +124,39 @@ struct RowsArgs {
   // Non-null: out = silu(gate) * (x . w), the gated MLP step in the epilogue
   // (gate: [m, out_dim] f32, the gate projection's output).
   const float* gate;
+  // Split over K (kparts > 1): chunk c is part c % kparts of row group
+  // c / kparts, slices [part * kslices, min(nslices, (part + 1) * kslices)).
+  uint32_t kparts, kslices, epoch;
+  unsigned long long* arrive;  // [n_rg] (epoch << 32) | parts arrived
+  uint32_t* part_special;      // [n_rg][kparts] non-finite row masks of the parts
+  float* part_sums;            // [kparts][m][out_dim] raw sums of the parts
 };
+
+// Counts a part in on its row group's arrival word; true for the last of
+// `parts` parts of launch `epoch`.  A count left under another epoch counts
+// as zero.  Relaxed: the parts exchange their sums and masks only through
+// agent-scope atomic stores and loads, which the caches do not hold back, and
+// the caller waits for its own stores to complete before it arrives -- no
+// fence, which would write back and invalidate the whole L2 of the XCD.
+__device__ __forceinline__ bool rows_arrive_last(unsigned long long* w, uint32_t epoch,
+                                                 uint32_t parts) {
+  unsigned long long old = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (;;) {  // at most `parts` rounds: a failed exchange means another part got in
+    const uint32_t cnt = (uint32_t)(old >> 32) == epoch ? (uint32_t)old + 1u : 1u;
+    const unsigned long long nw = ((unsigned long long)epoch << 32) | cnt;
+    if (__hip_atomic_compare_exchange_strong(w, &old, nw, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      return cnt == parts;
+  }
+}
+
+// Agent-scope relaxed store / load of a part's sum.
+__device__ __forceinline__ void part_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float part_load(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Units a wave holds per slice: four with IQ2_XXS's 5-register units, x read
 // as vectors and at most four result registers (up to 4 rows; W8A8 up to 8),
@@ -361,20 +408,25 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 
   float acc[kAcc];
   bool tables_ready = false;
+  uint32_t* s_last = reinterpret_cast<uint32_t*>(lds + a.flag_ofs + 4);  // last part (split)
   for (uint32_t chunk = blockIdx.x; chunk < a.nchunks; chunk += gridDim.x) {
     if (chunk != blockIdx.x) sync();  // the previous chunk's flags are read
-    row0 = (chunk * R + rgl) * 32;
-    crow0 = chunk * R * 32;
+    // row group chunk (of R row groups) and K part of this chunk
+    const uint32_t rgc = chunk / a.kparts, kpart = chunk - rgc * a.kparts;
+    const uint32_t s_begin = kpart * a.kslices;
+    const uint32_t s_end = min(a.nslices, s_begin + a.kslices);
+    row0 = (rgc * R + rgl) * 32;
+    crow0 = rgc * R * 32;
     const uint32_t code = !tables_ready ? F::seed(tid) : 0u;
     if (tid == 0) *s_special = 0;
     // set-up loads ahead of the weights: the first slice's activations, then a
     // barrier (which does not wait for loads), so that every wave's activation
     // requests are queued before any weight request
-    load_x(0);
-    load_scales(0);
+    load_x(s_begin);
+    load_scales(s_begin);
     sync();
 #pragma unroll
-    for (uint32_t t = 0; t < kEarly && t < kU; ++t) issue_unit(0, t);
+    for (uint32_t t = 0; t < kEarly && t < kU; ++t) issue_unit(s_begin, t);
     if (!tables_ready) {
       F::tables(lds, tid, code);
       tables_ready = true;
@@ -401,7 +453,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
 #pragma unroll
       for (uint32_t t = 0; t < kU; ++t) {
         // the first slice's later units: one more in flight per unit computed
-        if (s == 0 && t + kEarly < kU) issue_unit(0, t + kEarly);
+        if (s == s_begin && t + kEarly < kU) issue_unit(s_begin, t + kEarly);
         const uint32_t ul = wp + P * t;
         if (ul >= 2 * s_eff) break;  // uniform
         // the codes of the unit's 4 sub-blocks for this lane's row, and its scales
@@ -409,7 +461,7 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
         const typename F::Words w = F::unpack(q[t]);
         const float dq = F::unit_scale(q[t]);
         // the registers are free: prefetch (none after the last slice)
-        if (s + 1 < a.nslices) issue_unit(s + 1, t);
+        if (s + 1 < s_end) issue_unit(s + 1, t);
         float au[kT];
 #pragma unroll
         for (uint32_t tt = 0; tt < kT; ++tt) au[tt] = 0.0f;
@@ -427,7 +479,9 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
             for (uint32_t i = 0; i < kTO; ++i) {
               const uint32_t tt = kTO * o + i;
               const uint32_t hi = ((uint32_t)c[4 * i + 2] << 8) + (uint32_t)c[4 * i + 1];
-              const float f = (float)(int)((hi << 8) + (uint32_t)c[4 * i]);
+              const float f = F::kSplitSum
+                                  ? fmaf((float)(int)hi, 256.0f, (float)c[4 * i])
+                                  : (float)(int)((hi << 8) + (uint32_t)c[4 * i]);
               au[tt] = fmaf(f, scale * xs[tt], au[tt]);
             }
           }
@@ -495,8 +549,8 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
       }
     };
     sync();  // tables and the cleared flag
-    run_slice(0);
-    for (uint32_t s = 1; s < a.nslices; ++s) {
+    run_slice(s_begin);
+    for (uint32_t s = s_begin + 1; s < s_end; ++s) {
       load_x(s);
       load_scales(s);
       sync();  // the previous slice's digits and scales are consumed
@@ -504,7 +558,10 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
     }
 
     // ---- the P waves of a row group add their partial sums in wave order
-    const uint32_t chunk_row0 = chunk * R * 32;
+    // (split over K: into this part's sums in the workspace)
+    const uint32_t chunk_row0 = rgc * R * 32;
+    const bool split = a.kparts > 1;  // uniform
+    float* const psum = split ? a.part_sums + (size_t)kpart * a.m * a.out_dim : nullptr;
     uint32_t special = 0;
     bool gated = false;
     if constexpr (kW8A8) {
@@ -526,8 +583,12 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
           const uint32_t xrow = 8 * g + 4 * (ol >> 5) + i, row = chunk_row0 + rg * 32 + (ol & 31);
           if (xrow < a.m && row < a.out_dim) {
             const size_t oi = (size_t)xrow * a.out_dim + row;
-            const float v = sum * 0.125f / s_inv[xrow];  // q / inv, and the weights' 1/8
-            a.out[oi] = gated ? silu_mul(a.gate[oi], v) : v;
+            if (split) {
+              part_store(psum + oi, sum);
+            } else {
+              const float v = sum * 0.125f / s_inv[xrow];  // q / inv, and the weights' 1/8
+              a.out[oi] = gated ? silu_mul(a.gate[oi], v) : v;
+            }
           }
         }
       }
@@ -546,9 +607,45 @@ __global__ __launch_bounds__(kRowsThreads) void iq_gemv_rows_kernel(RowsArgs a) 
         const uint32_t xrow = 2 * tt + (ol >> 5), row = chunk_row0 + rg * 32 + (ol & 31);
         if (xrow < a.m && row < a.out_dim) {
           const size_t i = (size_t)xrow * a.out_dim + row;
-          a.out[i] = gated ? silu_mul(a.gate[i], sum) : sum;
+          if (split)
+            part_store(psum + i, sum);
+          else
+            a.out[i] = gated ? silu_mul(a.gate[i], sum) : sum;
         }
       }
+    }
+
+    // ---- split over K: hand the sums over; the last part of the row group
+    // to arrive adds every part's sums in part order and goes on with the
+    // outputs' fix-up (R = 1 when split)
+    if (split) {
+      const uint32_t nrow = min(32u, a.out_dim - chunk_row0);
+      if (tid == 0)
+        __hip_atomic_store(a.part_special + rgc * a.kparts + kpart, special, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      // every wave's stores of the sums complete (performed at agent scope)
+      // before the barrier, and the barrier before the arrival
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      sync();
+      if (tid == 0) *s_last = rows_arrive_last(a.arrive + rgc, a.epoch, a.kparts) ? 1u : 0u;
+      sync();
+      if (*s_last == 0) continue;  // uniform: another part finishes this row group
+      special = 0;
+      for (uint32_t k = 0; k < a.kparts; ++k)
+        special |= __hip_atomic_load(a.part_special + rgc * a.kparts + k, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+      gated = a.gate != nullptr && special == 0;
+      for (uint32_t o = tid; o < a.m * nrow; o += kRowsThreads) {
+        const uint32_t xrow = o / nrow, rl = o - xrow * nrow;
+        const size_t i = (size_t)xrow * a.out_dim + chunk_row0 + rl;
+        float sum = 0.0f;
+        for (uint32_t k = 0; k < a.kparts; ++k)
+          sum += part_load(a.part_sums + (size_t)k * a.m * a.out_dim + i);
+        if constexpr (kW8A8) sum = sum * 0.125f / s_inv[xrow];
+        a.out[i] = gated ? silu_mul(a.gate[i], sum) : sum;
+      }
+      if (tid == 0)
+        __hip_atomic_store(a.arrive + rgc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- rows that held a NaN or an infinity: add the kind of the
@@ -610,23 +707,82 @@ struct RowsPlan {
   uint32_t tasks;  // kTasks
   uint32_t rg_shift, nchunks, grid, slice_shift, nslices, plane_stride;
   uint32_t xdig_ofs, xsc_ofs, flag_ofs, sc_ofs;
+  uint32_t kparts, kslices;  // split over K
   size_t lds;
 };
 
 static uint32_t align16r(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Launch shape for m (1..8; W8A8 1..32) x out_dim x in_dim on num_cus CUs for
-// format F; false when the shape does not fit (31-bit buffer offsets, LDS).
+// Parts the split over K may cut each 32-row group into: the largest power of
+// two up to 8 that keeps the chunks within one per CU, with at least one
+// super-block per part (1: no split).  A function of the shape and the CU
+// count only, so the workspace query and the launch agree.
+static uint32_t rows_kparts_max(uint64_t out_dim, uint64_t in_dim, uint64_t cus) {
+  const uint64_t n_rg = (out_dim + 31) / 32, bpr = (in_dim + kQK - 1) / kQK;
+  uint32_t k = 1;
+  while (k < 8 && n_rg * (2 * k) <= cus && 2 * k <= bpr) k *= 2;
+  return k;
+}
+
+// Instantiation rows for m activation rows (the kernel's kRows).
+static uint32_t rows_for(uint32_t m, bool w8a8) {
+  return w8a8 ? (m <= 8 ? 8 : 32) : (m <= 2 ? 2 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16)));
+}
+
+// Whether splitting K in kmax parts shortens the launch.  The exchange of
+// the sums costs about three memory round trips (the sums' stores, the
+// arrival, the last part's loads: about 3 us at N = 4096) and more with more
+// parts (the arrivals retry against each other), so the split pays where a
+// workgroup's unsplit K loop is long: measured on MI355X (f32 x, mode Off and
+// W8A8, M = 2..32, N = 1024..4096, K = 2048..14336), splitting won for K >=
+// 12288 at any row count (N = 4096, K = 14336: 16.1 -> 13.4 us at M = 2),
+// for the 16-row (W8A8: 32-row) launches at K >= 8192, and for those at
+// K = 4096 with at most 4 parts (N = 4096 M = 16: 16.5 -> 13.8 us); it lost
+// 1-3 us at 2-8 rows with K <= 8192 (N = 4096, M = 4: 8.7 -> 10.4 us) and at
+// 8 parts with K = 4096 (N = 1024 M = 16: 16.0 -> 17.4 us).
+static bool rows_split_pays(uint32_t m, bool w8a8, uint32_t in_dim, uint32_t kmax) {
+  if (kmax < 2) return false;
+  const bool big = w8a8 ? rows_for(m, true) == 32 : rows_for(m, false) == 16;
+  return in_dim >= 12288 || (big && in_dim >= 8192) || (big && kmax <= 4 && in_dim >= 4096);
+}
+
+// Workspace of the split: arrival words, the parts' non-finite masks, then
+// the parts' sums for `rows` activation rows.
+static size_t rows_split_layout(uint32_t rows, uint32_t out_dim, uint32_t kmax,
+                                size_t* special_ofs, size_t* sums_ofs) {
+  const size_t n_rg = (out_dim + 31) / 32;
+  *special_ofs = align256(n_rg * sizeof(unsigned long long));
+  *sums_ofs = *special_ofs + align256(n_rg * kmax * sizeof(uint32_t));
+  return *sums_ofs + (size_t)kmax * rows * out_dim * sizeof(float);
+}
+
+size_t gemv_rows_split_bytes(uint32_t m, uint32_t out_dim, uint32_t in_dim, bool w8a8,
+                             int num_cus) {
+  if (m < 2 || out_dim == 0 || in_dim == 0) return 0;
+  const uint32_t kmax = rows_kparts_max(out_dim, in_dim, num_cus > 0 ? (uint64_t)num_cus : 1);
+  // (the largest launch of the call: later ones have no more rows, and the
+  // split pays for fewer rows only where it pays for more)
+  const uint32_t group = w8a8 ? 32 : 16;
+  const uint32_t rows = m < group ? m : group;
+  if (!rows_split_pays(rows, w8a8, in_dim, kmax)) return 0;
+  size_t so, mo;
+  return rows_split_layout(rows, out_dim, kmax, &so, &mo);
+}
+
+// Launch shape for m (1..16; W8A8 1..32) x out_dim x in_dim on num_cus CUs
+// for format F, split over K when `split` allows it; false when the shape
+// does not fit (31-bit buffer offsets, LDS).
 template <class F>
 static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, bool vec,
-                      bool w8a8, int num_cus, RowsPlan* p) {
+                      bool w8a8, int num_cus, bool split, RowsPlan* p) {
   if (m < 1 || m > (w8a8 ? 32u : 16u) || out_dim == 0 || in_dim == 0) return false;
   const uint64_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t esize = x_dtype == 0 ? 4 : 2;
   if ((uint64_t)out_dim * bpr * F::kBlockBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)out_dim * bpr * F::kScaleBytes > kOutOfRange - 4096) return false;
   if ((uint64_t)m * in_dim * esize > kOutOfRange - 4096) return false;
-  p->rows = w8a8 ? (m <= 8 ? 8 : 32) : (m <= 2 ? 2 : (m <= 4 ? 4 : (m <= 8 ? 8 : 16)));
+  p->rows = rows_for(m, w8a8);
   p->tasks = rows_tasks(p->rows, w8a8, m);
   // activation rows digitised per slice (W8A8 digitises the m rows only)
   const uint64_t task_rows = w8a8 ? m : p->rows;
@@ -636,15 +792,17 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   while (rs < 4 && (n_rg + (1u << rs) - 1) >> rs > cus) ++rs;
   p->rg_shift = rs;
   const uint64_t waves_per_rg = kRowsWaves >> rs;
-  p->nchunks = (uint32_t)((n_rg + (1u << rs) - 1) >> rs);
-  p->grid = p->nchunks < cus ? p->nchunks : (uint32_t)cus;
+  const uint64_t rg_chunks = (n_rg + (1u << rs) - 1) >> rs;
+  // (n_rg <= cus whenever kmax > 1, so R = 1 when split)
+  const uint32_t kmax = split ? rows_kparts_max(out_dim, in_dim, cus) : 1;
   // slice: a power of two of super-blocks, at most kU units per wave and two
-  // digitisation tasks per thread, whose digits fit in LDS beside the tables
+  // digitisation tasks per thread, whose digits fit in LDS beside the tables;
+  // split: at most bpr / kmax, so that every part holds at least one slice
   const uint64_t units = rows_units<F>((int)p->rows, vec, w8a8);
   uint32_t ss = 0;
   while (2 * (2ull << ss) <= units * waves_per_rg &&
          task_rows * (2ull << ss) * 32 <= p->tasks * kRowsThreads &&
-         (1ull << ss) < bpr)
+         (1ull << ss) < bpr && (2ull << ss) * kmax <= bpr)
     ++ss;
   for (;; --ss) {
     const uint64_t S = 1ull << ss;
@@ -665,7 +823,14 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
     if ((1ull << rs) * S > 8 * units) return false;
     p->sc_ofs = p->flag_ofs + rows_flag_bytes(p->rows);
     p->lds = p->sc_ofs + align16r((1ull << rs) * 32 * S * F::kScaleBytes);
-    if (p->lds <= kGemvLdsLimit) return true;
+    if (p->lds <= kGemvLdsLimit) {
+      p->kslices = (p->nslices + kmax - 1) / kmax;
+      p->kparts = (p->nslices + p->kslices - 1) / p->kslices;  // every part non-empty
+      const uint64_t chunks = rg_chunks * p->kparts;
+      p->nchunks = (uint32_t)chunks;
+      p->grid = chunks < cus ? (uint32_t)chunks : (uint32_t)cus;
+      return true;
+    }
     if (ss == 0) return false;
   }
 }
@@ -673,7 +838,7 @@ static bool plan_rows(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
 bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype,
                          bool w8a8) {
   RowsPlan p;
-  return plan_rows<RowsFmtXXS>(m, out_dim, in_dim, x_dtype, false, w8a8, 1, &p);
+  return plan_rows<RowsFmtXXS>(m, out_dim, in_dim, x_dtype, false, w8a8, 1, false, &p);
 }
 
 template <class F, int XD, bool V, bool Q, int ROWS, int TASKS>
@@ -708,17 +873,36 @@ static hipError_t launch_rows_v(const RowsArgs& a, const RowsPlan& p, bool w8a8,
                      : launch_rows_t<F, XD, V, false, 8, 2>(a, p, stream);
 }
 
-// One launch for m <= 16 rows (W8A8: m <= 32).
+// Launch epochs of the split over K: distinct per launch (a captured launch
+// keeps its own), never 0 (a cleared arrival word).
+static uint32_t next_rows_epoch() {
+  static std::atomic<uint32_t> counter{0};
+  for (;;) {
+    const uint32_t e = (counter.fetch_add(1) + 1u) * 2654435761u;  // odd multiplier: a bijection
+    if (e != 0) return e;
+  }
+}
+
+// One launch for m <= 16 rows (W8A8: m <= 32); split over K when the shape
+// leaves CUs idle and `split_ws` (16-byte aligned) holds split_ws_bytes >=
+// gemv_rows_split_bytes(m, ...).
 template <class F>
 static hipError_t launch_rows_fmt(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                   const uint8_t* ws, float* out, uint32_t out_dim,
                                   uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
-                                  const float* gate) {
+                                  const float* gate, void* split_ws, size_t split_ws_bytes) {
   const size_t esize = x_dtype == 0 ? 4 : 2;
   const bool vec = (in_dim % 8 == 0) && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                    ((size_t)in_dim * esize % 16 == 0);
+  const uint32_t kmax = rows_kparts_max(out_dim, in_dim, num_cus > 0 ? (uint64_t)num_cus : 1);
+  size_t special_ofs = 0, sums_ofs = 0;
+  const size_t split_need = rows_split_pays(m, w8a8, in_dim, kmax)
+                                ? rows_split_layout(m, out_dim, kmax, &special_ofs, &sums_ofs)
+                                : 0;
+  const bool split = split_need > 0 && split_ws != nullptr && split_ws_bytes >= split_need &&
+                     reinterpret_cast<uintptr_t>(split_ws) % 16 == 0;
   RowsPlan p;
-  if (!plan_rows<F>(m, out_dim, in_dim, x_dtype, vec, w8a8, num_cus, &p))
+  if (!plan_rows<F>(m, out_dim, in_dim, x_dtype, vec, w8a8, num_cus, split, &p))
     return hipErrorInvalidValue;
   RowsArgs a;
   a.x = x;
@@ -743,6 +927,13 @@ static hipError_t launch_rows_fmt(const void* x, int x_dtype, uint32_t m, const 
   a.flag_ofs = p.flag_ofs;
   a.sc_ofs = p.sc_ofs;
   a.gate = gate;
+  a.kparts = p.kparts;
+  a.kslices = p.kslices;
+  a.epoch = p.kparts > 1 ? next_rows_epoch() : 0u;
+  uint8_t* const wsb = static_cast<uint8_t*>(split_ws);
+  a.arrive = p.kparts > 1 ? reinterpret_cast<unsigned long long*>(wsb) : nullptr;
+  a.part_special = p.kparts > 1 ? reinterpret_cast<uint32_t*>(wsb + special_ofs) : nullptr;
+  a.part_sums = p.kparts > 1 ? reinterpret_cast<float*>(wsb + sums_ofs) : nullptr;
   switch (x_dtype) {
     case 0: return vec ? launch_rows_v<F, 0, true>(a, p, w8a8, stream)
                        : launch_rows_v<F, 0, false>(a, p, w8a8, stream);
@@ -756,18 +947,18 @@ static hipError_t launch_rows_fmt(const void* x, int x_dtype, uint32_t m, const 
 hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                    const uint8_t* ws, float* out, uint32_t out_dim,
                                    uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
-                                   const float* gate) {
+                                   const float* gate, void* split_ws, size_t split_ws_bytes) {
   return launch_rows_fmt<RowsFmtXXS>(x, x_dtype, m, wb, ws, out, out_dim, in_dim, w8a8, num_cus,
-                                     stream, gate);
+                                     stream, gate, split_ws, split_ws_bytes);
 }
 
 template <class F>
 static bool variant_rows_fit(uint32_t out_dim, uint32_t in_dim, int x_dtype) {
   RowsPlan p;
-  return plan_rows<F>(16, out_dim, in_dim, x_dtype, false, false, 1, &p) &&
-         plan_rows<F>(8, out_dim, in_dim, x_dtype, false, false, 1, &p) &&
-         plan_rows<F>(4, out_dim, in_dim, x_dtype, true, false, 1, &p) &&
-         plan_rows<F>(32, out_dim, in_dim, x_dtype, false, true, 1, &p);
+  return plan_rows<F>(16, out_dim, in_dim, x_dtype, false, false, 1, false, &p) &&
+         plan_rows<F>(8, out_dim, in_dim, x_dtype, false, false, 1, false, &p) &&
+         plan_rows<F>(4, out_dim, in_dim, x_dtype, true, false, 1, false, &p) &&
+         plan_rows<F>(32, out_dim, in_dim, x_dtype, false, true, 1, false, &p);
 }
 
 bool variant_rows_supported(int variant, uint32_t out_dim, uint32_t in_dim, int x_dtype) {
@@ -782,7 +973,7 @@ bool variant_rows_supported(int variant, uint32_t out_dim, uint32_t in_dim, int 
 hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint32_t m,
                                   const uint8_t* wb, const uint8_t* ws, float* out,
                                   uint32_t out_dim, uint32_t in_dim, bool w8a8, int num_cus,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, void* split_ws, size_t split_ws_bytes) {
   const size_t esize = x_dtype == 0 ? 4 : 2;
   // groups of 16 activation rows (W8A8: 32), each a launch that reads every
   // weight once
@@ -795,15 +986,18 @@ hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint3
     switch (variant) {
       case 1:
         e = launch_rows_fmt<RowsFmtXS>(xr, x_dtype, mr, wb, ws, o, out_dim, in_dim, w8a8,
-                                       num_cus, stream, nullptr);
+                                       num_cus, stream, nullptr, split_ws,
+                                       split_ws_bytes);
         break;
       case 2:
         e = launch_rows_fmt<RowsFmtS>(xr, x_dtype, mr, wb, ws, o, out_dim, in_dim, w8a8,
-                                      num_cus, stream, nullptr);
+                                      num_cus, stream, nullptr, split_ws,
+                                       split_ws_bytes);
         break;
       case 3:
         e = launch_rows_fmt<RowsFmtS3>(xr, x_dtype, mr, wb, ws, o, out_dim, in_dim, w8a8,
-                                       num_cus, stream, nullptr);
+                                       num_cus, stream, nullptr, split_ws,
+                                       split_ws_bytes);
         break;
       default:
         return hipErrorInvalidValue;

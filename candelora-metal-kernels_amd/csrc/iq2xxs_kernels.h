@@ -21,18 +21,29 @@ hipError_t launch_iq2xxs_dequant(const uint8_t* wb, const uint8_t* ws, void* out
 // 2 GB).  Needs 16-byte aligned weight_bytes and 2-byte aligned weight_scales.
 // gate non-null: out = silu(gate) * (x . w) with gate [m, out_dim] f32 (not
 // overlapping out), the gated MLP step in the epilogue.
+// split_ws: workspace of the multi-row kernel's split over K (16-byte
+// aligned, split_ws_bytes >= gemv_rows_split_bytes(m, ...)); without it the
+// kernel runs unsplit.
 bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype);
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream,
-                              const float* gate = nullptr);
+                              const float* gate = nullptr, void* split_ws = nullptr,
+                              size_t split_ws_bytes = 0);
 // The multi-row kernel alone (1 <= m <= 16; W8A8: 1 <= m <= 32).
 bool gemv_rows_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype,
                          bool w8a8 = false);
 hipError_t launch_iq2xxs_gemv_rows(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                                    const uint8_t* ws, float* out, uint32_t out_dim,
                                    uint32_t in_dim, bool w8a8, int num_cus, hipStream_t stream,
-                                   const float* gate = nullptr);
+                                   const float* gate = nullptr, void* split_ws = nullptr,
+                                   size_t split_ws_bytes = 0);
+// Workspace bytes the multi-row kernel's split over K uses for m rows (any
+// m: launches of up to 16 rows, W8A8 32, share it one after another) on
+// num_cus CUs; 0 where it does not split (m = 1, or the row groups fill the
+// CUs).  Any format: the split depends on the shape only.
+size_t gemv_rows_split_bytes(uint32_t m, uint32_t out_dim, uint32_t in_dim, bool w8a8,
+                             int num_cus);
 
 // W8A8 per-row inverse scale: inv[r] = 127 / max|x_r| (1 when max < 1e-8).
 hipError_t launch_iq2xxs_row_inv_scale(const void* x, int x_dtype, uint32_t m, uint32_t in_dim,
@@ -103,7 +114,8 @@ bool variant_rows_supported(int variant, uint32_t out_dim, uint32_t in_dim, int 
 hipError_t launch_iq_variant_rows(int variant, const void* x, int x_dtype, uint32_t m,
                                   const uint8_t* wb, const uint8_t* ws, float* out,
                                   uint32_t out_dim, uint32_t in_dim, bool w8a8, int num_cus,
-                                  hipStream_t stream);
+                                  hipStream_t stream, void* split_ws = nullptr,
+                                  size_t split_ws_bytes = 0);
 hipError_t launch_iq_variant_dequant(int variant, const uint8_t* wb, const uint8_t* ws, void* out,
                                      int out_kind, uint32_t out_dim, uint32_t in_dim, int num_cus,
                                      hipStream_t stream);

@@ -3,8 +3,11 @@
 // half a super-block), and the expansion of a lane's codes into signed int8
 // weights for the MFMA.
 //
-// Activation digits have F::kDigitShift bits: the int32 plane sums of one MFMA
-// must hold (columns) x 2^kDigitShift x (largest code magnitude).
+// Activation digits have F::kDigitShift bits (21: the widest the
+// magic-number digitisation gives, |rint| <= 2^21).  The plane sums of one
+// MFMA, (columns) x 2^kDigitShift x (largest code magnitude), are combined
+// in int32 where they stay below 2^31, and as 256 * (256 C2 + C1) + C0 with
+// one fp32 rounding otherwise (F::kSplitSum).
 //
 // Every format's weight is w = dl * g * sign with g a small odd or level
 // magnitude (IQ2: {8, 25, 43}; IQ3_S: odd 1..15) and dl = d * (2s+1) / 8
@@ -95,8 +98,11 @@ __device__ __forceinline__ uint32_t swap_lo(uint32_t v) {
 // ---------------------------------------------------------------------------
 struct RowsFmtXXS {
   static constexpr bool kHalf = false;
-  // activation digits of 20 bits: 32 columns x 2^20 x 43 stay below 2^31
-  static constexpr int kDigitShift = 20;
+  // activation digits of 21 bits: 32 columns x 2^21 x 43 pass 2^31, so the
+  // planes combine as 256 * (256 C2 + C1) + C0 (the inner sum exact in int32,
+  // below 2^24; one fp32 rounding, 2^-24 relative, against the digits' 2^-22)
+  static constexpr int kDigitShift = 21;
+  static constexpr bool kSplitSum = true;
   static constexpr uint32_t kTableBytes = GemvTables<true>::kBytes;
   static constexpr uint32_t kBlockBytes = 64, kScaleBytes = 2;
   struct Consts {
@@ -194,6 +200,7 @@ struct RowsFmtXS {
   static constexpr bool kHalf = true;
   // 21-bit digits: 16 columns x 2^21 x 43 stay below 2^31
   static constexpr int kDigitShift = 21;
+  static constexpr bool kSplitSum = false;
   static constexpr uint32_t kTableBytes = 80 * 1024;
   static constexpr uint32_t kBlockBytes = 64, kScaleBytes = 10;
   struct Consts {
@@ -291,6 +298,7 @@ struct RowsFmtXS {
 struct RowsFmtS {
   static constexpr bool kHalf = true;
   static constexpr int kDigitShift = 21;  // as IQ2_XS
+  static constexpr bool kSplitSum = false;
   static constexpr uint32_t kTableBytes = 96 * 1024;
   static constexpr uint32_t kBlockBytes = 72, kScaleBytes = 10;
   struct Consts {
@@ -391,6 +399,7 @@ struct RowsFmtS3 {
   // 21-bit digits: 32 columns x 2^21 x 15 stay below 2^31 (22 bits would let
   // rint reach 2^22, past the range of the magic-number digitisation)
   static constexpr int kDigitShift = 21;
+  static constexpr bool kSplitSum = false;
   static constexpr uint32_t kTableBytes = 96 * 1024;
   static constexpr uint32_t kBlockBytes = 104, kScaleBytes = 6;
   struct Consts {

@@ -218,11 +218,18 @@ def iq2_matmul_swiglu(x, weight_bytes, weight_scales, out_dim, in_dim, gate):
     g = gate.contiguous()
     out = torch.empty((m, out_dim), dtype=torch.float32, device=x.device)
     if m > 0:
+        xd = _DTYPES[x2.dtype]
+        # the workspace iq2_xxs_matmul takes (the multi-row kernel's split over
+        # K), so that both run the same launch
+        ws_bytes = cabi.workspace_size(xd, m, out_dim, in_dim)
+        work = (torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None)
         try:
-            cabi.matmul_swiglu_raw(x2.data_ptr(), _DTYPES[x2.dtype], x2.numel(), m,
+            cabi.matmul_swiglu_raw(x2.data_ptr(), xd, x2.numel(), m,
                                    weight_bytes.data_ptr(), weight_bytes.numel(),
                                    weight_scales.data_ptr(), weight_scales.numel(), out_dim,
-                                   in_dim, g.data_ptr(), g.numel(), out.data_ptr(), _stream(x))
+                                   in_dim, g.data_ptr(), g.numel(), out.data_ptr(),
+                                   work.data_ptr() if work is not None else None, ws_bytes,
+                                   _stream(x))
         except cabi.CmkError as e:
             raise Iq2MatmulError(str(e)) from None
     return out.squeeze(0) if squeeze else out

@@ -37,8 +37,8 @@ extern "C" {
                                  weight_bytes: *const u8, weight_bytes_len: usize,
                                  weight_scales: *const u8, weight_scales_len: usize,
                                  out_dim: usize, in_dim: usize, gate: *const f32,
-                                 gate_len: usize, out: *mut f32,
-                                 stream: *mut c_void) -> c_int;
+                                 gate_len: usize, out: *mut f32, workspace: *mut c_void,
+                                 workspace_bytes: usize, stream: *mut c_void) -> c_int;
     pub fn cmk_iq2_split_gguf_blocks(blocks: *const u8, blocks_len: usize, n_blocks: usize,
                                      variant: CmkVariant, weight_bytes: *mut u8,
                                      weight_bytes_len: usize, weight_scales: *mut u8,

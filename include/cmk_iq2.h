@@ -36,8 +36,12 @@ extern "C" {
 
 /* 2: cmk_iq2_matmul_noalloc and cmk_iq2_matmul_swiglu exported; f32 x at 9-16
  * rows and W8A8 at 17-32 rows run on the multi-row decode kernel, with the
- * workspace sizes that follow from it. */
-#define CMK_IQ2_ABI_VERSION 2
+ * workspace sizes that follow from it.
+ * 3: the multi-row decode kernel splits K over several workgroups when its
+ * row groups leave CUs idle, in an optional workspace that
+ * cmk_iq2_matmul_workspace_size now reports (m >= 2, N <= 4096 on 256 CUs);
+ * cmk_iq2_matmul_swiglu takes a workspace. */
+#define CMK_IQ2_ABI_VERSION 3
 
 /* Status codes. */
 typedef enum cmk_status {
@@ -103,6 +107,14 @@ typedef enum cmk_act_quant_mode {
  * scaled by a power of two and staged as an f16 head / tail pair, so x keeps
  * about 22 bits) and for shapes too small to fill the GPU, whose k is split
  * (partials summed in a fixed order: results are the same on every run).
+ * The multi-row decode kernel (2 <= m, decode shapes) uses the workspace when
+ * it is given and large enough, and runs without it otherwise: its 32-row
+ * groups fill at most N / 32 CUs, so where that leaves CUs idle it splits K
+ * into parts, one workgroup each, whose sums meet in the workspace and are
+ * added in part order by the part that finishes last (the same results on
+ * every run, equal to the unsplit launch up to fp32 rounding).  The workspace
+ * needs no initial contents; launches that share one must be ordered (one
+ * stream).
  */
 int cmk_iq2_matmul(const void *x, cmk_dtype x_dtype, size_t x_len, size_t m,
                    const uint8_t *weight_bytes, size_t weight_bytes_len,
@@ -136,7 +148,9 @@ int cmk_iq2_matmul_noalloc(const void *x, cmk_dtype x_dtype, size_t x_len, size_
 
 /* Device scratch (bytes) that cmk_iq2_matmul needs for these arguments.  The
  * launch never allocates; callers that get a non-zero size pass a buffer of at
- * least that many bytes.  Same argument validation as cmk_iq2_matmul. */
+ * least that many bytes.  Same argument validation as cmk_iq2_matmul.  The
+ * size includes the multi-row kernel's optional split over K, counted for
+ * 256 CUs (a device with fewer CUs never splits more). */
 int cmk_iq2_matmul_workspace_size(cmk_dtype x_dtype, size_t m, size_t out_dim, size_t in_dim,
                                   cmk_iq2_variant variant, cmk_act_quant_mode mode,
                                   size_t *bytes);
@@ -194,15 +208,17 @@ int cmk_swiglu(const float *gate, const float *up, size_t n, cmk_dtype out_dtype
  * epilogue evaluates the same fp32 expression on the same sum.  Serves the
  * decode-shaped kernels only (m <= 16, no
  * activation quantisation, weight_bytes 16-byte and weight_scales 2-byte
- * aligned); CMK_ERR_UNSUPPORTED otherwise.  No workspace.  No counterpart in
- * the reference, whose callers compose the MLP from candle ops.  Device
- * pointers, asynchronous on `stream`.
+ * aligned); CMK_ERR_UNSUPPORTED otherwise.  `workspace` as for cmk_iq2_matmul
+ * with mode OFF (cmk_iq2_matmul_workspace_size): the bit-for-bit equality
+ * holds between calls given the same workspace size (both split K or
+ * neither).  No counterpart in the reference, whose callers compose the MLP
+ * from candle ops.  Device pointers, asynchronous on `stream`.
  */
 int cmk_iq2_matmul_swiglu(const void *x, cmk_dtype x_dtype, size_t x_len, size_t m,
                           const uint8_t *weight_bytes, size_t weight_bytes_len,
                           const uint8_t *weight_scales, size_t weight_scales_len,
                           size_t out_dim, size_t in_dim, const float *gate, size_t gate_len,
-                          float *out, void *stream);
+                          float *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Errors and introspection                                                  */

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol(cabi):
     for s in syms:
         assert hasattr(L, s), s
     assert sorted(cabi.EXPORTED) == syms
-    assert L.cmk_abi_version() == 2
+    assert L.cmk_abi_version() == 3
 
 
 NULL = None
@@ -175,9 +175,34 @@ def test_workspace_and_path_queries(cabi):
     # 256 tiles (the M=512 prefill shape) or too few blocks: no split; bf16
     # rows are staged as scaled f16 (row scales + the rows) for f16 weights
     assert cabi.workspace_size(cabi.CMK_BF16, 17, 64, 320) == 256 + 17 * 320 * 2
-    # in_dim % 8 != 0 keeps f32 rows off the GEMM (portable path, no workspace)
+    # in_dim % 8 != 0 keeps f32 rows off the GEMM: the multi-row kernel in
+    # launches of 16 rows, too short a K to split
     assert cabi.matmul_path(cabi.CMK_F32, 64, 300, 1001) == "gemv"
     assert cabi.workspace_size(cabi.CMK_F32, 64, 300, 1001) == 0
+    # the multi-row kernel's split over K (optional workspace) where it pays:
+    # N = 4096 has 128 row groups of 32 on 256 CUs -> 2 parts, taken by the
+    # 16-row launches at K = 4096 (arrival words, part masks, the parts' sums)
+    # and by every launch at K >= 12288; N = 14336 fills the CUs
+    for m in (2, 4, 8):
+        assert cabi.workspace_size(cabi.CMK_F32, m, 4096, 4096) == 0
+    for m in (12, 16):
+        assert cabi.workspace_size(cabi.CMK_F32, m, 4096, 4096) == 1024 + 1024 + 2 * m * 4096 * 4
+    for m in (2, 8):
+        assert cabi.workspace_size(cabi.CMK_F32, m, 4096, 14336) == 1024 + 1024 + 2 * m * 4096 * 4
+    for m in (2, 16):
+        assert cabi.workspace_size(cabi.CMK_F32, m, 14336, 4096) == 0
+    # W8A8: the 32-row launches (m > 8) split at K = 4096, the 8-row ones not
+    assert (cabi.workspace_size(cabi.CMK_F32, 32, 4096, 4096, mode=cabi.CMK_ACT_QUANT_W8A8)
+            == 1024 + 1024 + 2 * 32 * 4096 * 4)
+    # (the 8-row ones: the portable path's row scales only, reported in case
+    # unaligned weights send the call there)
+    assert cabi.workspace_size(cabi.CMK_F32, 8, 4096, 4096, mode=cabi.CMK_ACT_QUANT_W8A8) == 256
+    # N = 1024: 32 row groups -> 8 parts, taken at K = 8192 by 16-row launches
+    assert cabi.workspace_size(cabi.CMK_F16, 16, 1024, 8192) == 256 + 1024 + 8 * 16 * 1024 * 4
+    assert cabi.workspace_size(cabi.CMK_F16, 16, 1024, 4096) == 0
+    # IQ2_XS rows take the same split
+    assert (cabi.workspace_size(cabi.CMK_F32, 16, 4096, 4096, variant=cabi.CMK_IQ2_XS)
+            == 1024 + 1024 + 2 * 16 * 4096 * 4)
     with pytest.raises(cabi.CmkError):
         cabi.workspace_size(cabi.CMK_F16, 1, 0, 4096)
 
