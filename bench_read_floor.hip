@@ -1,4 +1,4 @@
-// probe_read.hip — a plain read of n bytes from HBM: the floor bench.py sets
+// bench_read_floor.hip — a plain read of n bytes from HBM: the floor bench.py sets
 // beside the decode GEMV (the same bytes read, no decoding, no arithmetic).
 // Not part of the matmul library or its C ABI; built as libcmk_probe.so.
 //

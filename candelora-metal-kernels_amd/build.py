@@ -86,8 +86,8 @@ def build_lib() -> str:
 
 
 def build_probe() -> str:
-    """bench.py's plain-read kernel (csrc/probe_read.hip), a library of its own."""
-    obj = _compile(os.path.join(CSRC, "probe_read.hip"))
+    """bench.py's plain-read kernel (bench_read_floor.hip beside it), a library of its own."""
+    obj = _compile(os.path.join(REPO, "bench_read_floor.hip"))
     tmp = PROBE_LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, obj])
     os.replace(tmp, PROBE_LIB)
