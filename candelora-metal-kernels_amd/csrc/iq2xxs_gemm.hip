@@ -770,10 +770,13 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(const float4* _
 }
 
 // Tile shape and k split of one launch.  256 x 112 tiles halve the
-// dequantisation per CU and are used when they still give most CUs a tile,
-// and for 129-256 rows (one row block, where 128-row tiles would decode every
-// weight twice); when the tiles cannot fill half of the 256 CUs, k is split
-// (at least two blocks per split) until they do.
+// dequantisation per CU and are used, above 128 rows, when they still give
+// most CUs a tile, and for 129-256 rows (one row block, where 128-row tiles
+// would decode every weight twice).  Up to 128 rows one 128-row block holds
+// them all: 256-row tiles would run half their MFMAs on padding rows (config
+// 4's gate / up at M = 128, f16 x: 97 us on 256 x 112 tiles).  When the tiles
+// cannot fill half of the 256 CUs, k is split (at least two blocks per split)
+// until they do.
 struct GemmPlan {
   bool wide;  // 256 x 112 tiles (else 128 x 128)
   uint32_t splits, split_blocks;
@@ -783,7 +786,7 @@ static GemmPlan plan_gemm(uint32_t rows, uint32_t out_dim, uint32_t in_dim) {
   GemmPlan p;
   const uint32_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t t256 = (uint64_t)((rows + 255) / 256) * ((out_dim + 111) / 112);
-  p.wide = t256 >= 192 || (rows > 128 && rows <= 256);
+  p.wide = rows > 128 && (t256 >= 192 || rows <= 256);
   const uint64_t tiles = p.wide ? t256 : (uint64_t)((rows + 127) / 128) * ((out_dim + 127) / 128);
   uint64_t splits = 1;
   if (tiles <= 128 && bpr >= 4) splits = std::min<uint64_t>(256 / tiles, bpr / 2);

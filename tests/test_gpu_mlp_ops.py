@@ -120,11 +120,12 @@ def test_matmul_swiglu_equals_matmul_then_swiglu(pkg, inputs, dev, m, k, n, dtyp
         assert got1.shape == (n,) and torch.equal(got1, ref[0])
 
 
-@pytest.mark.parametrize("m", [1, 2])
-def test_matmul_swiglu_nonfinite(pkg, inputs, dev, m):
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 1024), (2, 4096, 1024), (4, 14336, 4096)])
+def test_matmul_swiglu_nonfinite(pkg, inputs, dev, m, k, n):
     """A NaN activation (the set-aside fix-up path) and a NaN / infinite gate
-    reach the output as through the matmul then swiglu."""
-    k, n = 4096, 1024
+    reach the output as through the matmul then swiglu (K = 14336 at N = 4096:
+    the multi-row kernel splits K, and the last part applies the gate after
+    the fix-up)."""
     wu, su = inputs.synthetic_weights(n, k, seed=31)
     wut, sut = torch.from_numpy(wu).to(dev), torch.from_numpy(su).to(dev)
     x = torch.from_numpy(inputs.synthetic_x(m, k, seed=32)).to(dev)
