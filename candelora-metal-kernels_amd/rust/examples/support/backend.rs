@@ -1,10 +1,9 @@
-// Backend selection for examples/iq2_matmul_bench.rs (`--backend metal|hip`),
-// to be added as examples/backend.rs and included with `mod backend;`.  The
-// bench parses the flag with `Backend::from_arg`, creates its device with
-// `Backend::device`, and keeps its timed loop unchanged.  With `hip` the device
-// is the CPU: the `rocm` bodies of src/iq2_matmul.rs stage the tensors into
-// device buffers per call, so these latencies include PCIe copies; bench.py in
-// the HIP build reports device-resident throughput.  Not built here.
+// Backend selection (`--backend metal|hip`) for examples/iq2_matmul_bench.rs,
+// which includes it with `#[path = "support/backend.rs"] mod backend;`: `Backend::from_arg` parses the
+// flag and `Backend::device` creates the device.  With `hip` the device is the
+// CPU: the `rocm` bodies of src/iq2_matmul.rs stage the tensors into device
+// buffers per call, so the example's latencies include PCIe copies; bench.py
+// reports the device-resident throughput of the same C ABI.  Not built here.
 use candle_core::{Device, Result};
 
 #[derive(Clone, Copy, Debug, PartialEq, Eq)]
