@@ -64,7 +64,8 @@ def test_bad_arguments_fail(fake_cargo, args):
 def test_example_accepts_every_option_the_script_passes():
     src = open(os.path.join(RUST, "examples", "iq2_matmul_bench.rs")).read()
     script = open(SCRIPT).read()
-    passed = set(re.findall(r"(--[a-z-]+) \"\$\{", script.split("cargo run", 1)[1]))
+    example_args = script.split("--example iq2_matmul_bench --", 1)[1]
+    passed = set(re.findall(r"(--[a-z-]+) \"\$\{", example_args))
     handled = set(re.findall(r'"(--[a-z-]+)" =>', src))
     assert passed and passed <= handled, passed - handled
     assert '#[path = "support/backend.rs"]' in src
