@@ -58,6 +58,13 @@ DECODE_SHAPES = [("gate", 4096, 14336), ("up", 4096, 14336), ("down", 14336, 409
 # Untimed decode steps replayed right before the timed replay (about 7 ms of
 # work at the current speed), so the timed steps run at steady-state clocks.
 DECODE_WARM_STEPS = 300
+DECODE_STAT_REPLAYS = 10
+
+
+def nearest_rank(sorted_values, p):
+    """Nearest-rank percentile of sorted values (as the reference's bench)."""
+    rank = max(1, math.ceil(p * len(sorted_values)))
+    return sorted_values[min(rank, len(sorted_values)) - 1]
 
 
 def load_package():
@@ -287,13 +294,71 @@ def bench_decode(pkg, torch, stream, steps, warmup):
     ms = replay_timed(torch, cabi, graph, sh, steps, DECODE_WARM_STEPS)
     step_bytes = sum(alg_bytes(1, k, n) for _, k, n in DECODE_SHAPES)
     launches = steps * len(DECODE_SHAPES)
+    # the spread over further timed replays of the same graph (each after an
+    # untimed one): median and p95 of their mean launch times
+    per_replay = sorted(replay_timed(torch, cabi, graph, sh, steps, 1) * 1e3 / launches
+                        for _ in range(DECODE_STAT_REPLAYS))
     return {
         "ms": ms,
         "step_bytes": step_bytes,
         "launches": launches,
         "mean_launch_us": ms * 1e3 / launches,
         "per_launch_bytes": step_bytes / len(DECODE_SHAPES),
+        "launch_us_over_replays": {"replays": DECODE_STAT_REPLAYS,
+                                   "median": nearest_rank(per_replay, 0.50),
+                                   "p95": nearest_rank(per_replay, 0.95),
+                                   "min": per_replay[0], "max": per_replay[-1]},
     }
+
+
+def bench_reference_workload(pkg, torch, stream, warmup=5, runs=20, m=1, n=4096, k=4096):
+    """The reference bench's default workload and timing, for continuity with
+    it (examples/iq2_matmul_bench.rs:103-118 defaults, 251-324 per format):
+    every format at M=1, N=K=4096, f16 x, its LCG inputs (seeds xor'ed with
+    the dims, every d = 1.0), one weight set (resident in the caches, as
+    there).  Each run is one launch followed by a device synchronize, after
+    `warmup` such runs; it is timed twice: on the host around launch +
+    synchronize, as the reference times it, and by HIP events on the launch
+    stream (the kernel alone).  mean / p50 / p95 (nearest rank) in ms and
+    matmuls per second from the host mean, the reference's columns."""
+    cabi, inputs = pkg.cabi, pkg.inputs
+    dev = torch.device("cuda:0")
+    sh = int(stream.cuda_stream)
+    res = {}
+    for v, name in enumerate(("iq2-xxs", "iq2-xs", "iq2-s", "iq3-s")):
+        x, wb, ws = inputs.reference_bench_case_variant(v, m, n, k)
+        xt = torch.from_numpy(x).to(dev).to(torch.float16)
+        wbt, wst = torch.from_numpy(wb).to(dev), torch.from_numpy(ws).to(dev)
+        out = torch.empty((m, n), dtype=torch.float32, device=dev)
+        call = Matmul(cabi, xt, wbt, wst, out, m, k, n, cabi.CMK_F16, sh, variant=v)
+        start, stop = cabi.Event(), cabi.Event()
+        for _ in range(warmup):
+            call()
+            torch.cuda.synchronize()
+        host, device = [], []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            start.record(sh)
+            call()
+            stop.record(sh)
+            torch.cuda.synchronize()
+            host.append((time.perf_counter() - t0) * 1e3)
+            device.append(start.elapsed_ms(stop))
+        row = {}
+        for label, times in (("host", host), ("device", device)):
+            mean = sum(times) / len(times)
+            times.sort()
+            row[label] = {"mean_ms": mean, "p50_ms": nearest_rank(times, 0.50),
+                          "p95_ms": nearest_rank(times, 0.95)}
+        hm = row["host"]["mean_ms"]
+        row["matmuls_per_s"] = 1e3 / hm if hm > 0 else 0.0
+        res[name] = row
+        log(f"[bench] reference workload {name}: host mean {hm * 1e3:.1f} us "
+            f"(p95 {row['host']['p95_ms'] * 1e3:.1f}), kernel mean "
+            f"{row['device']['mean_ms'] * 1e3:.2f} us (p95 {row['device']['p95_ms'] * 1e3:.2f})")
+    res["workload"] = (f"examples/iq2_matmul_bench.rs defaults: m={m}, out_dim={n}, in_dim={k}, "
+                       f"f16 x, LCG inputs (d = 1), warmup {warmup}, runs {runs}")
+    return res
 
 
 def bench_read_floor(pkg, torch, stream, steps):
@@ -784,6 +849,7 @@ def main():
         variants = (None if args.no_variants
                     else bench_variants(pkg, torch, stream, args.variant_steps))
         split = None if args.no_variants else bench_gguf_split(pkg, torch, stream, 50)
+        refw = None if args.no_variants else bench_reference_workload(pkg, torch, stream)
         mlp = None if args.no_variants else bench_mlp_step(pkg, torch, stream, 300)
         configs = None if args.no_configs else bench_configs(pkg, torch, stream)
     torch.cuda.synchronize()
@@ -813,6 +879,7 @@ def main():
                      "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false, 0> "
                                "(XT = 1 for K=4096, 2 for K=14336)",
                      "mean_launch_us": dec["mean_launch_us"],
+                     "launch_us_over_replays": dec["launch_us_over_replays"],
                      "alg_bytes_per_launch": dec["per_launch_bytes"],
                      "read_floor": floor},
     }
@@ -822,6 +889,8 @@ def main():
         line["variants_m1"] = variants
     if split is not None:
         line["gguf_split"] = split
+    if refw is not None:
+        line["reference_bench_workload"] = refw
     if mlp is not None:
         line["mlp_step_m1"] = mlp
     if configs is not None:

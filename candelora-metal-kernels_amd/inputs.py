@@ -91,6 +91,24 @@ def reference_bench_case(m, out_dim, in_dim):
                           scales_seed=(0xC0FFEE12 ^ in_dim) & 0xFFFFFFFF)
 
 
+# bytes of codes / scales per 256-weight block of each format (src/iq2_matmul.rs:13-29)
+VARIANT_BLOCK_SIZES = {0: (64, 2), 1: (64, 10), 2: (72, 10), 3: (104, 6)}
+
+
+def reference_bench_case_variant(variant, m, out_dim, in_dim):
+    """examples/iq2_matmul_bench.rs:257-273 for any format: LCG codes and
+    scales (seeds xor'ed with the dims) sized by the format's block sizes,
+    every block's d = f16 1.0, the last code byte 0x5A, deterministic x."""
+    bpb, spb = VARIANT_BLOCK_SIZES[variant]
+    nb = out_dim * (-(-in_dim // QK))
+    wb = lcg_fill(nb * bpb, (0xA11CE5ED ^ out_dim) & 0xFFFFFFFF)
+    ws = force_f16_one_per_block(lcg_fill(nb * spb, (0xC0FFEE12 ^ in_dim) & 0xFFFFFFFF), spb)
+    if wb.size:
+        wb[-1] = 0x5A
+    x = deterministic_x(m * in_dim).reshape(m, in_dim)
+    return x, wb, ws
+
+
 # ---------------------------------------------------------------- splitmix64
 
 def splitmix64(seed: int, start: int, n: int) -> np.ndarray:
