@@ -227,21 +227,25 @@ __device__ __forceinline__ float qdq_w8a8(float x, float inv_scale) {
 // Activation digits for the int8 MFMA GEMV.
 //
 // A 32-column chunk of activations with max|x| < 2^e is mapped to integers
-// v = rint(x * 2^(20-e)), |v| <= 2^20.  The rounding is one fma against the
-// magic constant 1.5*2^23: the sum's mantissa holds 0x400000 + v exactly.
+// v = rint(x * 2^(D-e)), |v| <= 2^D (IQ2_XXS: D = kDigitShift = 22, the
+// other formats 21).  The rounding is one fma against the magic constant
+// 1.5*2^23: for |v| <= 2^22 the sum lies in [2^23, 2^24] and its bits are
+// bits(1.5*2^23) + v exactly (v = 2^22 carries into the exponent field).
 // u = v + 0x808080 is a 24-bit unsigned value whose bytes b0,b1,b2 give signed
 // digits s_k = b_k - 128 (the bytes of D = u ^ 0x808080 read as int8) with
 //     v = 65536*s2 + 256*s1 + s0      exactly,
 // so sum_k v_k w_k = 65536*C2 + 256*C1 + C0 with C_p = sum_k s_p,k w_k, the
 // three integer dot products the MFMA forms from three digit planes.  Over a
-// 32-column sub-block with |w| <= 43 the sum stays below 32*43*2^20 < 2^31.
-// The chunk scale 2^(e-20) is kept as a float per chunk.
+// 32-column sub-block with |w| <= 43 and D = 22 the sum passes 2^31
+// (32*43*2^22), so the kernels form 256*C2 + C1 in int32 and add C0 in fp32.
+// The chunk scale 2^(e-D) is kept as a float per chunk.
 // ---------------------------------------------------------------------------
-constexpr int kDigitShift = 20;
+constexpr int kDigitShift = 22;
 constexpr float kDigitMagic = 12582912.0f;       // 1.5 * 2^23
-constexpr uint32_t kDigitBias = 0x4ABF7F80u;     // bits(1.5*2^23) - 0x400000 - 0x808080 + 2^32
+constexpr uint32_t kDigitBias = 0x4ABF7F80u;     // bits(1.5*2^23) - 0x808080
 
-// Clamp of the chunk exponent so 2^(20-e) and 2^(e-23) stay finite and normal.
+// Clamp of the chunk exponent so 2^(D-e) and 2^(e-D-3) stay finite and normal
+// for digit widths D <= 22.
 __device__ __forceinline__ int digit_exponent(float max_abs) {
   int e;
   (void)frexpf(max_abs, &e);
@@ -249,7 +253,7 @@ __device__ __forceinline__ int digit_exponent(float max_abs) {
 }
 
 // The three digit bytes of x (bits 0..23) each plus 128, for chunk scale
-// 2^(20-e): the bytes of v + 0x808080.
+// 2^(D-e): the bytes of v + 0x808080.
 __device__ __forceinline__ uint32_t digitize_biased(float x, float scale) {
   const uint32_t bits = __float_as_uint(fmaf(x, scale, kDigitMagic));
   return bits - kDigitBias;

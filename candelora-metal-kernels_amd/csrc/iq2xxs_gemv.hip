@@ -15,7 +15,7 @@
 //
 // Arithmetic.
 //  * Activations become exact integer digits: each 32-column chunk with
-//    max|x| < 2^e gives v = rint(x*2^(20-e)) split into three signed 8-bit
+//    max|x| < 2^e gives v = rint(x*2^(22-e)) split into three signed 8-bit
 //    digit planes (iq2xxs_device.h), held in LDS.
 //  * Codes expand through two LDS tables: a codebook row holds 16 copies of
 //    {g, -g} (8 magnitude bytes and their negations), a sign row 16 copies of
@@ -25,8 +25,9 @@
 //  * v_mfma_i32_4x4x4_16b_i8: in each of the 16 4x4 blocks the A rows are the
 //    three digit planes (the fourth row is unused) and the B columns are 4 weight
 //    rows; eight instructions give, for 4 rows, the three digit sums of a
-//    32-column sub-block, combined exactly in int32 (|sum| < 2^31).  The scale
-//    d*(2s+1)/8 * 2^(e-20) is applied in fp32.
+//    32-column sub-block, combined as 256 * (256 C2 + C1) + C0 (the inner sum
+//    exact in int32, then two fp32 roundings of 2^-24 relative, against the
+//    digits' 2^-23).  The scale d*(2s+1)/8 * 2^(e-22) is applied in fp32.
 //  * A wave sums its 16 blocks with DPP and lane-swap moves; the workgroup
 //    adds the slices of a row in slice order.  Results are deterministic.
 //  * W8A8 (true int8): the reference's q = clamp(round(x * inv), +-127) is
@@ -91,10 +92,18 @@ __device__ __forceinline__ uint32_t sign_addr(uint32_t aux_s, uint32_t cs) {
 }
 
 // 65536 c[2] + 256 c[1] + c[0] in 32-bit arithmetic (exact when the result
-// fits in an int32).
+// fits in an int32: the 21-bit digits of the other formats).
 __device__ __forceinline__ int plane_sum(v4i c) {
   const uint32_t hi = ((uint32_t)c[2] << 8) + (uint32_t)c[1];
   return (int)((hi << 8) + (uint32_t)c[0]);
+}
+
+// The same sum in fp32 for the 22-bit IQ2_XXS digits, where it can pass
+// 2^31 (32 x 43 x 2^22): 256 c[2] + c[1] exactly in int32 (|c[2]| <= 32 x 64
+// x 43), then converted and added to c[0] with one fma.
+__device__ __forceinline__ float plane_sum_f(v4i c) {
+  const uint32_t hi = ((uint32_t)c[2] << 8) + (uint32_t)c[1];
+  return fmaf((float)(int)hi, 256.0f, (float)c[0]);
 }
 
 // Sum over the 16 lanes that share lane & 3 (the 16 4x4 blocks) of one
@@ -689,11 +698,10 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       c[0] = mfma4x4((int)xr[0][kk], (int)w[0][kk], c[0]);
       c[1] = mfma4x4((int)xr[1][kk], (int)w[1][kk], c[1]);
     }
-    // c[h][p] = sum over the 32 columns of digit plane p times w; the exact
-    // integer dot product 65536 c2 + 256 c1 + c0 of a sub-block stays below
-    // 2^31 in magnitude (32 * 43 * 2^20)
-    const float f0 = (float)plane_sum(c[0]);
-    const float f1 = (float)plane_sum(c[1]);
+    // c[h][p] = sum over the 32 columns of digit plane p times w; the
+    // sub-block's dot product 65536 c2 + 256 c1 + c0 (W8A8: c0 alone)
+    const float f0 = plane_sum_f(c[0]);
+    const float f1 = plane_sum_f(c[1]);
     // (2s+1) * 2^27 for the sub-block scale s in bits 28-31 of aux_s: the
     // conversion of s * 2^28 + 2^27 - 1 rounds to (2s+1) * 2^27 exactly (one
     // v_and_or with the low constant in a register: a VOP3 takes one literal)

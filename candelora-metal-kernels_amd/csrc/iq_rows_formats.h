@@ -3,11 +3,12 @@
 // half a super-block), and the expansion of a lane's codes into signed int8
 // weights for the MFMA.
 //
-// Activation digits have F::kDigitShift bits (21: the widest the
-// magic-number digitisation gives, |rint| <= 2^21).  The plane sums of one
-// MFMA, (columns) x 2^kDigitShift x (largest code magnitude), are combined
-// in int32 where they stay below 2^31, and as 256 * (256 C2 + C1) + C0 with
-// one fp32 rounding otherwise (F::kSplitSum).
+// Activation digits have F::kDigitShift bits (at most 22, the widest the
+// magic-number digitisation gives: |rint| <= 2^22 keeps fma(x, 2^(D-e),
+// 1.5 * 2^23) in [2^23, 2^24], where its bits are 0x4B400000 + rint).  The
+// plane sums of one MFMA, (columns) x 2^kDigitShift x (largest code
+// magnitude), are combined in int32 where they stay below 2^31, and as
+// 256 * (256 C2 + C1) + C0 in fp32 otherwise (F::kSplitSum).
 //
 // Every format's weight is w = dl * g * sign with g a small odd or level
 // magnitude (IQ2: {8, 25, 43}; IQ3_S: odd 1..15) and dl = d * (2s+1) / 8
@@ -98,10 +99,11 @@ __device__ __forceinline__ uint32_t swap_lo(uint32_t v) {
 // ---------------------------------------------------------------------------
 struct RowsFmtXXS {
   static constexpr bool kHalf = false;
-  // activation digits of 21 bits: 32 columns x 2^21 x 43 pass 2^31, so the
-  // planes combine as 256 * (256 C2 + C1) + C0 (the inner sum exact in int32,
-  // below 2^24; one fp32 rounding, 2^-24 relative, against the digits' 2^-22)
-  static constexpr int kDigitShift = 21;
+  // activation digits of 22 bits: 32 columns x 2^22 x 43 pass 2^31, so the
+  // planes combine as 256 * (256 C2 + C1) + C0: the inner sum is exact in
+  // int32 (|C2| <= 32 x 64 x 43, below 2^25) and is converted and added to C0
+  // with two fp32 roundings of 2^-24 relative, against the digits' 2^-23
+  static constexpr int kDigitShift = 22;
   static constexpr bool kSplitSum = true;
   static constexpr uint32_t kTableBytes = GemvTables<true>::kBytes;
   static constexpr uint32_t kBlockBytes = 64, kScaleBytes = 2;
