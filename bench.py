@@ -440,11 +440,11 @@ def bench_prefill(pkg, torch, stream, steps, warmup, m=512, k=4096, n=14336):
 # IQ2_XS, IQ2_S, IQ3_S: (ABI variant, bytes, scales per 256-weight block, the
 # kernel that serves them at M=1)
 VARIANTS = [("iq2_xs", 1, 64, 10,
-             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 1> (one-row GEMV, IQ2_XS)"),
+             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 1, false> (one-row GEMV, IQ2_XS)"),
             ("iq2_s", 2, 72, 10,
-             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 2> (one-row GEMV, IQ2_S)"),
+             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 2, false> (one-row GEMV, IQ2_S)"),
             ("iq3_s", 3, 104, 6,
-             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 3> (one-row GEMV, IQ3_S)")]
+             "cmk::iq2xxs_gemv_kernel<0, true, true, 1, false, false, 3, false> (one-row GEMV, IQ3_S)")]
 
 
 def bench_variants(pkg, torch, stream, steps, k=4096, n=14336):
@@ -876,7 +876,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "traffic_source": traffic_source,
-                     "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false, 0> "
+                     "kernel": "cmk::iq2xxs_gemv_kernel<0, true, true, XT, false, false, 0, false> "
                                "(XT = 1 for K=4096, 2 for K=14336)",
                      "mean_launch_us": dec["mean_launch_us"],
                      "launch_us_over_replays": dec["launch_us_over_replays"],

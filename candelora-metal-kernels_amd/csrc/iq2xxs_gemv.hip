@@ -1,5 +1,8 @@
 // iq2xxs_gemv.hip — decode-shaped IQ2_XXS matmul, one activation row, for
-// gfx950 (more rows: iq2xxs_gemv_rows.hip).
+// gfx950; also 2 to 4 rows where the multi-row kernel (iq2xxs_gemv_rows.hip,
+// which serves more rows) would leave CUs idle (out_dim <= 16 per CU): the
+// rows then take the places of the digit planes in the MFMA's A operand
+// (kM4, below).
 //
 // Replaces iq2_xxs_matmul_kernel / iq2_xxs_matmul_w8a8_kernel
 // (src/metal_src/iq2_matmul.metal:188-240, 436-499), which run one thread per
@@ -71,6 +74,8 @@ namespace cmk {
 __device__ __forceinline__ v4i mfma4x4(int a_xdigits, int b_weights, v4i c) {
   return __builtin_amdgcn_mfma_i32_4x4x4i8(a_xdigits, b_weights, c, 0, 0, 0);
 }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kGemvWaves = 16;
 constexpr uint32_t kGemvThreads = kGemvWaves * 64;
@@ -159,7 +164,9 @@ struct GemvArgs {
   uint32_t nslices;       // tiles per row group = ceil(npairs / 16)
   uint32_t rg_per_chunk;  // row groups per chunk
   uint32_t nchunks;
-  uint32_t ntasks;        // digitisation tasks per activation row (8 columns each)
+  uint32_t ntasks;        // digitisation tasks (8 columns each): m * ntasks_row
+  uint32_t ntasks_row;    // digitisation tasks per activation row
+  uint32_t ntasks_magic;  // ceil(2^32 / ntasks_row): t / ntasks_row = umulhi(t, magic), t < 2^11
   uint32_t wb_records, ws_records, x_records;  // bytes addressable by the buffer loads
   uint32_t plane_stride;  // LDS bytes between the three digit planes
   uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs, flag_ofs;  // LDS layout
@@ -191,12 +198,20 @@ struct GemvArgs {
 // tile as IQ2_XXS, dl = d (2s+1) and 21-bit digits (32 x 2^21 x 15 < 2^31).
 constexpr int kGemvXXS = 0, kGemvXS = 1, kGemvS = 2, kGemvS3 = 3;
 
-template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti, int kFmt = kGemvXXS>
+// kM4: 2 to 4 activation rows (IQ2_XXS, one chunk per workgroup, every
+// digitisation task in registers at once): A row j of the MFMA is activation
+// row j instead of digit plane j, one chain pair per digit plane (W8A8: one
+// plane, q), and a lane's four results are the four rows' sums for its weight
+// row.  The weights are still decoded once per launch.
+template <int XD, bool kVecX, bool kWide, int kXT, bool kW8A8, bool kMulti, int kFmt = kGemvXXS,
+          bool kM4 = false>
 __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   constexpr bool kXS = kFmt == kGemvXS, kS = kFmt == kGemvS, kS3 = kFmt == kGemvS3;
   constexpr bool kH16 = kXS || kS;  // a sub-scale per 16 weights, 10 scale bytes per block
   constexpr bool kOther = kFmt != kGemvXXS;
   static_assert(!kOther || (kWide && !kMulti), "other formats: wide tables, one chunk per workgroup");
+  static_assert(!kM4 || (!kOther && !kMulti), "2 to 4 rows: IQ2_XXS, one chunk per workgroup");
+  constexpr uint32_t kP = kW8A8 ? 1 : 3;  // digit planes per activation row (kM4 layout)
   extern __shared__ __align__(16) uint8_t lds[];
   using TL = GemvTables<kWide>;
   constexpr int kDS = kOther ? RowsFmtXS::kDigitShift : kDigitShift;  // digit bits
@@ -385,8 +400,15 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (uint32_t u = 0; u < (uint32_t)kXT; ++u) {
       const uint32_t task = r0 + u * kGemvThreads + rtid;
-      const uint32_t c0 = (task >> 2) * 32 + (task & 3) * 8;
-      xo[u].load(rx, mrow * a.in_dim + c0, c0, a.in_dim, task < a.ntasks && c0 < a.in_dim);
+      if constexpr (kM4) {
+        // task = row * ntasks_row + tr over all the rows
+        const uint32_t row = __umulhi(task, a.ntasks_magic), tr = task - row * a.ntasks_row;
+        const uint32_t c0 = (tr >> 2) * 32 + (tr & 3) * 8;
+        xo[u].load(rx, row * a.in_dim + c0, c0, a.in_dim, task < a.ntasks && c0 < a.in_dim);
+      } else {
+        const uint32_t c0 = (task >> 2) * 32 + (task & 3) * 8;
+        xo[u].load(rx, mrow * a.in_dim + c0, c0, a.in_dim, task < a.ntasks && c0 < a.in_dim);
+      }
     }
   };
   // W8A8 row scale (iq2_matmul.metal:86-96) from the row's values in xo (the
@@ -502,6 +524,113 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
       for (uint32_t r0 = round; r0 < a.ntasks; r0 += round) {
         load_x(r0, mrow);
         digitize_round(r0, inv_row, gen);
+      }
+    }
+  };
+  // kM4: the W8A8 scale of each of the (up to 4) rows, from the values in xo;
+  // ends in a barrier.  Layout: digit plane p of row r at (r * kP + p) *
+  // plane_stride, chunk scales of row r at xsc[r * 8 * bpr ...].
+  // (four variables, not an array: selects between array elements by a
+  // lane's row index get turned into a scratch table)
+  float inv4_0 = 1.0f, inv4_1 = 1.0f, inv4_2 = 1.0f, inv4_3 = 1.0f;
+  auto inv_of = [&](uint32_t r) {
+    return r == 0 ? inv4_0 : (r == 1 ? inv4_1 : (r == 2 ? inv4_2 : inv4_3));
+  };
+  auto w8a8_inv4 = [&]() {
+    float mx[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t u = 0; u < (uint32_t)kXT; ++u) {
+      const uint32_t row = __umulhi(u * kGemvThreads + rtid, a.ntasks_magic);
+      float v = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v = fmaxf(v, fabsf(xo[u].get(k)));
+#pragma unroll
+      for (uint32_t r = 0; r < 4; ++r) mx[r] = row == r ? fmaxf(mx[r], v) : mx[r];
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) mx[r] = fmaxf(mx[r], __shfl_xor(mx[r], off));
+      if (lane == 0) s_wred[r * kGemvWaves + wave] = mx[r];
+    }
+    __syncthreads();
+    float inv[4];
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+      float m = 0.0f;
+#pragma unroll
+      for (uint32_t w = 0; w < kGemvWaves; ++w) m = fmaxf(m, s_wred[r * kGemvWaves + w]);
+      inv[r] = (m < 1e-8f) ? 1.0f : 127.0f / m;
+    }
+    inv4_0 = inv[0];
+    inv4_1 = inv[1];
+    inv4_2 = inv[2];
+    inv4_3 = inv[3];
+  };
+  // kM4: digits of every row from the tasks in xo (as digitize_round; a
+  // non-finite value sets bit `row` of s_special).
+  auto digitize4 = [&]() {
+    const uint32_t nsb = a.bpr * 8;
+#pragma unroll
+    for (uint32_t u = 0; u < (uint32_t)kXT; ++u) {
+      const uint32_t task = u * kGemvThreads + rtid;
+      const uint32_t row = __umulhi(task, a.ntasks_magic), tr = task - row * a.ntasks_row;
+      const bool ok = task < a.ntasks;
+      const float inv = kW8A8 ? inv_of(row) : 1.0f;
+      float xv[8], qv[8];
+      uint32_t mb = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        xv[k] = xo[u].get(k);
+        if constexpr (kW8A8) xv[k] = qv[k] = quant_w8a8(xv[k], inv);
+      }
+      if constexpr (kW8A8) {
+        if (inv < 0x1p-100f) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) xv[k] = qv[k] / inv;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) mb = max(mb, __float_as_uint(xv[k]) & kAbsMask);
+      mb = quad_max_u32(mb);
+      if (mb >= kInfBits) {
+        mb = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t ab = __float_as_uint(xv[k]) & kAbsMask;
+          if (ab >= kInfBits) {
+            xv[k] = 0.0f;
+            if constexpr (kW8A8) qv[k] = 0.0f;
+          }
+          mb = max(mb, ab < kInfBits ? ab : 0u);
+        }
+        mb = quad_max_u32(mb);
+        if (ok) atomicOr(s_special, 1u << row);
+      }
+      if (!ok) continue;
+      const uint32_t c0 = (tr >> 2) * 32 + (tr & 3) * 8;
+      uint8_t* const dst = xdig + row * kP * a.plane_stride + c0;
+      if constexpr (kW8A8) {
+        uint32_t qb[2] = {0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qb[k >> 2] |= ((uint32_t)(int)qv[k] & 0xFFu) << (8 * (k & 3));
+        *reinterpret_cast<uint2*>(dst) = make_uint2(qb[0], qb[1]);
+        if ((tr & 3) == 0) xsc[row * nsb + (tr >> 2)] = 0.125f;
+      } else {
+        const int e = digit_exponent(__uint_as_float(mb));
+        const float scale = ldexpf(1.0f, kDS - e);
+        uint32_t dg[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dg[k] = digitize_biased(xv[k], scale);
+        uint32_t p0[2], p1[2], p2[2];
+        digits_to_planes(dg[0], dg[1], dg[2], dg[3], p0[0], p1[0], p2[0]);
+        digits_to_planes(dg[4], dg[5], dg[6], dg[7], p0[1], p1[1], p2[1]);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(p0[0] ^ 0x80808080u, p0[1] ^ 0x80808080u);
+        *reinterpret_cast<uint2*>(dst + a.plane_stride) =
+            make_uint2(p1[0] ^ 0x80808080u, p1[1] ^ 0x80808080u);
+        *reinterpret_cast<uint2*>(dst + 2 * a.plane_stride) =
+            make_uint2(p2[0] ^ 0x80808080u, p2[1] ^ 0x80808080u);
+        if ((tr & 3) == 0) xsc[row * nsb + (tr >> 2)] = ldexpf(1.0f, e - kDS - 3);
       }
     }
   };
@@ -710,6 +839,77 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     const float ud1 = (float)((words[3] & 0xF0000000u) | k27) * d;
     return fmaf(f1 * ud1, xs[1], (f0 * ud0) * xs[0]);
   };
+  // kM4: this lane's partials of tile k for activation rows 0..3 (before the
+  // sum over the 16 blocks).  A row j is activation row j (rows past m read
+  // zeros); per digit plane, from the highest, two chains of eight MFMAs, and
+  // the planes combine as ((C2 * 256 + C1) * 256 + C0) in fp32 (two roundings
+  // of 2^-24 relative).  The digits are read per tile: the three planes of a
+  // row do not fit in registers next to the rest.
+  auto compute_tile4 = [&](uint32_t k) -> f32x4 {
+    const uint32_t pair = min(tslice[k] * kSlicePairs + b, a.npairs - 1);
+    const uint32_t nsb = a.bpr * 8;
+    const bool arow = j < a.m;
+    const uint32_t jrow = min(j, a.m - 1);
+    const uint32_t words[4] = {q[k].x, q[k].y, q[k].z, q[k].w};
+    uint32_t w[2][8];
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+      const uint32_t aux_g = words[2 * h];
+      const uint32_t aux_s = words[2 * h + 1];
+      const uint32_t ga[4] = {perm_addr<0>(aux_g, cg), perm_addr<1>(aux_g, cg),
+                              perm_addr<2>(aux_g, cg), perm_addr<3>(aux_g, cg)};
+      const uint32_t sa[4] = {sign_addr<kWide, 0>(aux_s, cs), sign_addr<kWide, 1>(aux_s, cs),
+                              sign_addr<kWide, 2>(aux_s, cs), sign_addr<kWide, 3>(aux_s, cs)};
+      u32x4 gv[4];
+      u32x2 sm[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        gv[g] = lds_u4(ga[g]);
+        sm[g] = lds_u2(sa[g]);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        w[h][2 * g] = bit_select(sm[g].x, gv[g].z, gv[g].x);
+        w[h][2 * g + 1] = bit_select(sm[g].y, gv[g].w, gv[g].y);
+      }
+    }
+    float f[2][4];
+#pragma unroll
+    for (int p = (int)kP - 1; p >= 0; --p) {
+      uint32_t xa[2][8];
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            xdig + (jrow * kP + (uint32_t)p) * a.plane_stride + (2 * pair + h) * 32);
+        const u32x4 lo = src[0], hi = src[1];
+        xa[h][0] = lo.x; xa[h][1] = lo.y; xa[h][2] = lo.z; xa[h][3] = lo.w;
+        xa[h][4] = hi.x; xa[h][5] = hi.y; xa[h][6] = hi.z; xa[h][7] = hi.w;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) xa[h][kk] = arow ? xa[h][kk] : 0u;
+      }
+      v4i c[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        c[0] = mfma4x4((int)xa[0][kk], (int)w[0][kk], c[0]);
+        c[1] = mfma4x4((int)xa[1][kk], (int)w[1][kk], c[1]);
+      }
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h)
+#pragma unroll
+        for (uint32_t r = 0; r < 4; ++r)
+          f[h][r] = p == (int)kP - 1 ? (float)c[h][r] : fmaf(f[h][r], 256.0f, (float)c[h][r]);
+    }
+    const float d = dsc[k];
+    const float ud0 = (float)((words[1] & 0xF0000000u) | k27) * d;
+    const float ud1 = (float)((words[3] & 0xF0000000u) | k27) * d;
+    f32x4 res;
+#pragma unroll
+    for (uint32_t r = 0; r < 4; ++r) {
+      const float* xs_r = xsc + min(r, a.m - 1) * nsb + 2 * pair;
+      res[r] = fmaf(f[1][r] * ud1, xs_r[1], (f[0][r] * ud0) * xs_r[0]);
+    }
+    return res;
+  };
   // Adds the set-aside terms of activation row mrow (NaN or infinite x) to the
   // chunk's outputs: every thread scans its columns of x; for each such column
   // it forms x_c * w_rc for the chunk's rows and records the kind of the term.
@@ -747,7 +947,45 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   };
   // Row sums of the chunk's tiles for activation row mrow, into out.
   static_assert(kTilesPerWave == 4, "sum_over_blocks4 reduces four tiles");
+  f32x4 acc4[kM4 ? kTilesPerWave : 1];
   auto reduce_and_store = [&](uint32_t mrow) {
+    if constexpr (kM4) {
+      // per tile: lane l then holds activation row l >> 4, weight row l & 3
+      const uint32_t rgc = a.rg_per_chunk;
+#pragma unroll
+      for (uint32_t k = 0; k < kTilesPerWave; ++k) {
+        if (k >= cnt) break;  // uniform
+        const float v = sum_over_blocks4(acc4[k][0], acc4[k][1], acc4[k][2], acc4[k][3]);
+        if ((lane & 12) == 0 && (lane >> 4) < a.m)
+          red[(((lane >> 4) * rgc + trgl[k]) * a.nslices + tslice[k]) * 4 + j] = v;
+      }
+      sync();
+      const uint32_t special = *s_special;  // bit r: row r held a non-finite value (uniform)
+      for (uint32_t r = 0; r < a.m; ++r) {
+        const bool gated = a.gate != nullptr && !((special >> r) & 1u);
+        for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
+          const float* p = red + ((r * rgc + (rl >> 2)) * a.nslices) * 4 + (rl & 3);
+          float sum = 0.0f;
+          for (uint32_t sl = 0; sl < a.nslices; ++sl) sum += p[sl * 4];
+          const size_t o = (size_t)r * a.out_dim + row_begin + rl;
+          const float v = kW8A8 ? sum / inv_of(r) : sum;  // W8A8: q / inv
+          a.out[o] = gated ? silu_mul(a.gate[o], v) : v;
+        }
+      }
+      for (uint32_t r = 0; r < a.m; ++r) {
+        if (!((special >> r) & 1u)) continue;  // uniform
+        inv_row = inv_of(r);
+        fix_up_special(r);
+        if (a.gate != nullptr) {
+          // (each thread rereads the outputs it wrote)
+          for (uint32_t rl = tid; rl < rows; rl += kGemvThreads) {
+            const size_t o = (size_t)r * a.out_dim + row_begin + rl;
+            a.out[o] = silu_mul(a.gate[o], a.out[o]);
+          }
+        }
+      }
+      return;
+    }
     if constexpr (!kMulti) {
       // acc[k] is 0 for k >= cnt
       const float v = sum_over_blocks4(acc[0], acc[1], acc[2], acc[3]);
@@ -822,7 +1060,12 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
                           TL::kSignCopies / 2);
   }
   __builtin_amdgcn_sched_barrier(0);
-  digitize_row(0);
+  if constexpr (kM4) {
+    if constexpr (kW8A8) w8a8_inv4();
+    digitize4();
+  } else {
+    digitize_row(0);
+  }
   stage_scales();
   // the rest of the first tiles, then a barrier that leaves them in flight
   // (the set-up loads were consumed above; the tiles are the last loads issued)
@@ -845,7 +1088,12 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     if (k + kTilesAhead < kTilesPerWave) q[k + kTilesAhead] = load_tile(k + kTilesAhead);
     __builtin_amdgcn_sched_barrier(0);
-    if (k < cnt) acc[k] = compute_tile(k);  // uniform
+    if constexpr (kM4) {
+      acc4[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (k < cnt) acc4[k] = compute_tile4(k);  // uniform
+    } else {
+      if (k < cnt) acc[k] = compute_tile(k);  // uniform
+    }
     if constexpr (kMulti) {
       // tile k's registers are free: the next chunk's scales (once), then its tile k
       if (next < a.nchunks) {
@@ -885,7 +1133,7 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
 // Launch policy.
 // ---------------------------------------------------------------------------
 struct GemvPlan {
-  uint32_t nslices, rg_per_chunk, nchunks, grid, ntasks, xt, plane_stride;
+  uint32_t nslices, rg_per_chunk, nchunks, grid, ntasks, ntasks_row, xt, plane_stride;
   uint32_t scale_ofs, xsc_ofs, xdig_ofs, red_ofs, wred_ofs, flag_ofs;
   size_t lds;
   bool wide;
@@ -898,9 +1146,12 @@ static uint32_t align16(uint64_t v) { return (uint32_t)((v + 15) & ~15ull); }
 // sb_bytes / scale_loads: scale bytes per block and staged scale dwords per
 // thread (IQ2_XS: 10 and 3).
 // table_bytes: a format's fixed table size (0: the IQ2_XXS wide or narrow layout).
+// xrows / planes: activation rows digitised and digit planes per row (the
+// 2-4 row kernel: m and 3, W8A8 1; else 1 and 3).
 static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, int num_cus,
                       GemvPlan* p, uint32_t sb_bytes = kScalesPerBlock,
-                      uint32_t scale_loads = kScaleLoads, uint32_t table_bytes = 0) {
+                      uint32_t scale_loads = kScaleLoads, uint32_t table_bytes = 0,
+                      uint32_t xrows = 1, uint32_t planes = 3) {
   const uint64_t bpr = (in_dim + kQK - 1) / kQK;
   const uint64_t npairs = bpr * 4;
   const uint64_t nsb = bpr * 8;
@@ -931,24 +1182,28 @@ static bool plan_gemv(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype
   p->rg_per_chunk = (uint32_t)rg_per_chunk;
   p->nchunks = (uint32_t)((n_rg + rg_per_chunk - 1) / rg_per_chunk);
   p->grid = p->nchunks < cus ? p->nchunks : (uint32_t)cus;
-  p->ntasks = (uint32_t)(nsb * 4);
+  p->ntasks_row = (uint32_t)(nsb * 4);
+  p->ntasks = p->ntasks_row * xrows;
   // two rounds' worth of activations per thread at most (more would spill);
   // longer rows digitise in further rounds
   p->xt = p->ntasks <= kGemvThreads ? 1 : 2;
   p->plane_stride = (uint32_t)(nsb * 32 + 16);
   const uint64_t scale_bytes = align16(rg_per_chunk * 4 * nslices * (kSlicePairs / 4) * sb_bytes);
-  const uint64_t rest = scale_bytes + align16(nsb * 4) + 3ull * p->plane_stride +
-                        align16(rg_per_chunk * nslices * 16) + kGemvWaves * 4 + 16;
+  // per-wave maxima of the W8A8 row scales: one row, or four (the 2-4 row kernel)
+  const uint32_t wred_bytes = kGemvWaves * 4 * (xrows > 1 ? 4 : 1);
+  const uint64_t rest = scale_bytes + align16(xrows * nsb * 4) +
+                        (uint64_t)planes * xrows * p->plane_stride +
+                        align16(xrows * rg_per_chunk * nslices * 16) + wred_bytes + 16;
   p->wide = (table_bytes ? table_bytes : GemvTables<true>::kBytes) + rest <= kGemvLdsLimit;
   if (table_bytes && !p->wide) return false;
   const uint32_t tb =
       table_bytes ? table_bytes : (p->wide ? GemvTables<true>::kBytes : GemvTables<false>::kBytes);
   p->scale_ofs = tb;
   p->xsc_ofs = p->scale_ofs + (uint32_t)scale_bytes;
-  p->xdig_ofs = p->xsc_ofs + align16(nsb * 4);
-  p->red_ofs = p->xdig_ofs + 3 * p->plane_stride;
-  p->wred_ofs = p->red_ofs + align16(rg_per_chunk * nslices * 16);
-  p->flag_ofs = p->wred_ofs + kGemvWaves * 4;
+  p->xdig_ofs = p->xsc_ofs + align16(xrows * nsb * 4);
+  p->red_ofs = p->xdig_ofs + planes * xrows * p->plane_stride;
+  p->wred_ofs = p->red_ofs + align16(xrows * rg_per_chunk * nslices * 16);
+  p->flag_ofs = p->wred_ofs + wred_bytes;
   p->lds = p->flag_ofs + 16;
   return p->lds <= kGemvLdsLimit;
 }
@@ -961,19 +1216,19 @@ bool gemv_supported(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype) 
   return plan_gemv(m, out_dim, in_dim, x_dtype, 1, &p);
 }
 
-template <int XD, bool V, bool W, int XT, bool Q, bool M, int F = kGemvXXS>
+template <int XD, bool V, bool W, int XT, bool Q, bool M, int F = kGemvXXS, bool M4 = false>
 static hipError_t launch_gemv_t(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
   // The tables alone exceed the default 64 KB of dynamic LDS: raise the
   // limit once per instantiation.
   static std::atomic<bool> attr_set{false};
   if (!attr_set.load()) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, F>),
+        reinterpret_cast<const void*>(&iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, F, M4>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemvLdsLimit);
     if (e != hipSuccess) return e;
     attr_set.store(true);
   }
-  hipLaunchKernelGGL((iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, F>), dim3(p.grid),
+  hipLaunchKernelGGL((iq2xxs_gemv_kernel<XD, V, W, XT, Q, M, F, M4>), dim3(p.grid),
                      dim3(kGemvThreads), p.lds, stream, a);
   return hipGetLastError();
 }
@@ -1026,6 +1281,8 @@ static GemvArgs gemv_args(const void* x, int x_dtype, uint32_t m, const uint8_t*
   a.rg_per_chunk = p.rg_per_chunk;
   a.nchunks = p.nchunks;
   a.ntasks = p.ntasks;
+  a.ntasks_row = p.ntasks_row;
+  a.ntasks_magic = (uint32_t)((0x100000000ull + p.ntasks_row - 1) / p.ntasks_row);
   a.wb_records = out_dim * a.bpr * block_bytes;
   a.ws_records = out_dim * a.bpr * sb_bytes;
   a.x_records = m * in_dim * (x_dtype == 0 ? 4u : 2u);
@@ -1117,10 +1374,66 @@ hipError_t launch_iq_variant_gemv(int variant, const void* x, int x_dtype, const
   }
 }
 
+// 2 to 4 activation rows on the one-row kernel (kM4): rows of x 16-byte
+// aligned, every digitisation task in registers at once (m * 32 * bpr <=
+// 2048), one chunk per workgroup and the LDS budget.
+static bool plan_gemv4(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtype, bool w8a8,
+                       const void* x, int num_cus, GemvPlan* p) {
+  const size_t esize = x_dtype == 0 ? 4 : 2;
+  if (m < 2 || m > 4 || in_dim % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 ||
+      (size_t)in_dim * esize % 16 != 0)
+    return false;
+  if (!plan_gemv(m, out_dim, in_dim, x_dtype, num_cus, p, kScalesPerBlock, kScaleLoads, 0, m,
+                 w8a8 ? 1 : 3))
+    return false;
+  return p->nchunks <= p->grid && p->ntasks <= kGemvThreads * p->xt;
+}
+
+// Where the 2-4 row launch runs instead of the multi-row kernel: where the
+// latter's 32-row groups would cover at most half the CUs (out_dim <= 16 per
+// CU, 4096 on 256).  Timed side by side on MI355X (graph replays, rotated
+// weights, f32 x; f16 alike): N = 4096, K = 4096, m = 2 / 3 / 4: 6.20 / 6.75 /
+// 7.09 against 7.45 / 8.21 / 8.45 us; N = 1024: 4.9 / 5.6 / 6.1 against 7.1 /
+// 8.0 / 8.2 us; N = 4096, K = 2048: 5.0 / 5.2 / 5.5 against 6.4 / 6.6 / 6.7
+// us; W8A8 within 4 % either way at these N.  At N = 14336 (K = 4096) it lost
+// (m = 4: 12.0 against 10.5 us), as at N = 8192 (K = 8192, m = 2: 13.2
+// against 10.8 us): the three MFMA chains per tile and the per-tile digit
+// reads then outweigh the fuller grid.
+static bool gemv4_pays(uint32_t out_dim, int num_cus) {
+  return (uint64_t)out_dim <= 16ull * (uint64_t)(num_cus > 0 ? num_cus : 1);
+}
+
+template <int XD, bool W, bool Q>
+static hipError_t launch_gemv4_xt(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
+  return p.xt <= 1 ? launch_gemv_t<XD, true, W, 1, Q, false, kGemvXXS, true>(a, p, stream)
+                   : launch_gemv_t<XD, true, W, 2, Q, false, kGemvXXS, true>(a, p, stream);
+}
+
+template <int XD>
+static hipError_t launch_gemv4(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
+  if (a.w8a8)
+    return p.wide ? launch_gemv4_xt<XD, true, true>(a, p, stream)
+                  : launch_gemv4_xt<XD, false, true>(a, p, stream);
+  return p.wide ? launch_gemv4_xt<XD, true, false>(a, p, stream)
+                : launch_gemv4_xt<XD, false, false>(a, p, stream);
+}
+
 hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint8_t* wb,
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream, const float* gate,
                               void* split_ws, size_t split_ws_bytes) {
+  if (m > 1 && m <= 4 && gemv4_pays(out_dim, num_cus)) {
+    GemvPlan p;
+    if (plan_gemv4(m, out_dim, in_dim, x_dtype, w8a8, x, num_cus, &p)) {
+      const GemvArgs a = gemv_args(x, x_dtype, m, wb, ws, out, out_dim, in_dim, w8a8, gate, p,
+                                   kScalesPerBlock);
+      switch (x_dtype) {
+        case 0: return launch_gemv4<0>(a, p, stream);
+        case 1: return launch_gemv4<1>(a, p, stream);
+        default: return launch_gemv4<2>(a, p, stream);
+      }
+    }
+  }
   if (m > 1) {
     // groups of up to 16 activation rows (W8A8: 32), each decoding the weights once
     const size_t esize = x_dtype == 0 ? 4 : 2;
