@@ -57,8 +57,9 @@ typedef enum cmk_status {
 typedef enum cmk_dtype { CMK_F32 = 0, CMK_F16 = 1, CMK_BF16 = 2 } cmk_dtype;
 
 /* Iq2MatmulVariant (src/iq2_matmul.rs:31-37).  All four are implemented.  IQ2_XXS
- * runs on the one-row GEMV (m = 1), the multi-row decode kernel (up to 16 rows per
- * launch, W8A8 32) and the MFMA GEMM (larger m).  IQ2_XS / IQ2_S / IQ3_S run on the
+ * runs on the one-row GEMV (m = 1, and 2-4 rows where out_dim <= 16 per CU), the
+ * multi-row decode kernel (up to 16 rows per launch, W8A8 32) and the MFMA GEMM
+ * (larger m).  IQ2_XS / IQ2_S / IQ3_S run on the
  * one-row GEMV at m = 1 and on the multi-row decode kernel otherwise when the
  * buffers are aligned (weight_bytes 16-byte or 8-byte, weight_scales 2-byte), and
  * on a byte-load kernel for any other alignment.  Bytes / scales per 256-weight
