@@ -873,6 +873,54 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         w[h][2 * g + 1] = bit_select(sm[g].y, gv[g].w, gv[g].y);
       }
     }
+    const float d = dsc[k];
+    const float ud0 = (float)((words[1] & 0xF0000000u) | k27) * d;
+    const float ud1 = (float)((words[3] & 0xF0000000u) | k27) * d;
+    if (!kW8A8 && a.m <= 2) {  // uniform
+      // Two rows: the six (row, plane) pairs in two A operands, A row j of
+      // the first = plane j >> 1 of row j & 1, of the second = plane 2 of row
+      // j (j < 2), so two chain pairs per tile instead of three.
+      float f2[2][2];
+#pragma unroll
+      for (int set = 1; set >= 0; --set) {
+        const uint32_t row = j & 1, plane = set ? 2u : (j >> 1);
+        const bool valid = (set ? j < 2 : true) && row < a.m;
+        const uint32_t rr = min(row, a.m - 1);
+        uint32_t xa[2][8];
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h) {
+          const u32x4* src = reinterpret_cast<const u32x4*>(
+              xdig + (rr * kP + plane) * a.plane_stride + (2 * pair + h) * 32);
+          const u32x4 lo = src[0], hi = src[1];
+          xa[h][0] = lo.x; xa[h][1] = lo.y; xa[h][2] = lo.z; xa[h][3] = lo.w;
+          xa[h][4] = hi.x; xa[h][5] = hi.y; xa[h][6] = hi.z; xa[h][7] = hi.w;
+#pragma unroll
+          for (int kk = 0; kk < 8; ++kk) xa[h][kk] = valid ? xa[h][kk] : 0u;
+        }
+        v4i c[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          c[0] = mfma4x4((int)xa[0][kk], (int)w[0][kk], c[0]);
+          c[1] = mfma4x4((int)xa[1][kk], (int)w[1][kk], c[1]);
+        }
+        // first pass: plane 2 of rows 0, 1 (C rows 0, 1); second: planes 0
+        // and 1 of row r in C rows r and 2 + r
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h)
+#pragma unroll
+          for (uint32_t r = 0; r < 2; ++r)
+            f2[h][r] = set ? (float)c[h][r]
+                           : fmaf(fmaf(f2[h][r], 256.0f, (float)c[h][2 + r]), 256.0f,
+                                  (float)c[h][r]);
+      }
+      f32x4 res2 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t r = 0; r < 2; ++r) {
+        const float* xs_r = xsc + min(r, a.m - 1) * nsb + 2 * pair;
+        res2[r] = fmaf(f2[1][r] * ud1, xs_r[1], (f2[0][r] * ud0) * xs_r[0]);
+      }
+      return res2;
+    }
     float f[2][4];
 #pragma unroll
     for (int p = (int)kP - 1; p >= 0; --p) {
@@ -899,9 +947,6 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
         for (uint32_t r = 0; r < 4; ++r)
           f[h][r] = p == (int)kP - 1 ? (float)c[h][r] : fmaf(f[h][r], 256.0f, (float)c[h][r]);
     }
-    const float d = dsc[k];
-    const float ud0 = (float)((words[1] & 0xF0000000u) | k27) * d;
-    const float ud1 = (float)((words[3] & 0xF0000000u) | k27) * d;
     f32x4 res;
 #pragma unroll
     for (uint32_t r = 0; r < 4; ++r) {
@@ -1391,15 +1436,20 @@ static bool plan_gemv4(uint32_t m, uint32_t out_dim, uint32_t in_dim, int x_dtyp
 
 // Where the 2-4 row launch runs instead of the multi-row kernel: where the
 // latter's 32-row groups would cover at most half the CUs (out_dim <= 16 per
-// CU, 4096 on 256).  Timed side by side on MI355X (graph replays, rotated
+// CU, 4096 on 256), and for two rows (two MFMA chain pairs per tile) at any
+// out_dim when K <= 4096.  Timed side by side on MI355X (graph replays, rotated
 // weights, f32 x; f16 alike): N = 4096, K = 4096, m = 2 / 3 / 4: 6.20 / 6.75 /
 // 7.09 against 7.45 / 8.21 / 8.45 us; N = 1024: 4.9 / 5.6 / 6.1 against 7.1 /
 // 8.0 / 8.2 us; N = 4096, K = 2048: 5.0 / 5.2 / 5.5 against 6.4 / 6.6 / 6.7
 // us; W8A8 within 4 % either way at these N.  At N = 14336 (K = 4096) it lost
 // (m = 4: 12.0 against 10.5 us), as at N = 8192 (K = 8192, m = 2: 13.2
 // against 10.8 us): the three MFMA chains per tile and the per-tile digit
-// reads then outweigh the fuller grid.
-static bool gemv4_pays(uint32_t out_dim, int num_cus) {
+// reads then outweigh the fuller grid.  Two rows, with their six (row, plane)
+// pairs packed into two A operands: N = 14336, K = 4096 9.7 (f16 x 8.8, W8A8
+// 10.7) against 10.3 (10.2, 12.0) us; N = 4096 5.6 against 6.1 us (6.0
+// unpacked); N = 8192, K = 8192 level or 3 % slower (f32, W8A8).
+static bool gemv4_pays(uint32_t m, uint32_t out_dim, uint32_t in_dim, int num_cus) {
+  if (m <= 2 && in_dim <= 4096) return true;
   return (uint64_t)out_dim <= 16ull * (uint64_t)(num_cus > 0 ? num_cus : 1);
 }
 
@@ -1422,7 +1472,7 @@ hipError_t launch_iq2xxs_gemv(const void* x, int x_dtype, uint32_t m, const uint
                               const uint8_t* ws, float* out, uint32_t out_dim, uint32_t in_dim,
                               bool w8a8, int num_cus, hipStream_t stream, const float* gate,
                               void* split_ws, size_t split_ws_bytes) {
-  if (m > 1 && m <= 4 && gemv4_pays(out_dim, num_cus)) {
+  if (m > 1 && m <= 4 && gemv4_pays(m, out_dim, in_dim, num_cus)) {
     GemvPlan p;
     if (plan_gemv4(m, out_dim, in_dim, x_dtype, w8a8, x, num_cus, &p)) {
       const GemvArgs a = gemv_args(x, x_dtype, m, wb, ws, out, out_dim, in_dim, w8a8, gate, p,

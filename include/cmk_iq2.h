@@ -57,13 +57,14 @@ typedef enum cmk_status {
 typedef enum cmk_dtype { CMK_F32 = 0, CMK_F16 = 1, CMK_BF16 = 2 } cmk_dtype;
 
 /* Iq2MatmulVariant (src/iq2_matmul.rs:31-37).  All four are implemented.  IQ2_XXS
- * runs on the one-row GEMV (m = 1, and 2-4 rows where out_dim <= 16 per CU), the
- * multi-row decode kernel (up to 16 rows per launch, W8A8 32) and the MFMA GEMM
- * (larger m).  IQ2_XS / IQ2_S / IQ3_S run on the
- * one-row GEMV at m = 1 and on the multi-row decode kernel otherwise when the
- * buffers are aligned (weight_bytes 16-byte or 8-byte, weight_scales 2-byte), and
- * on a byte-load kernel for any other alignment.  Bytes / scales per 256-weight
- * block: 64/2, 64/10, 72/10, 104/6 (src/iq2_matmul.rs:13-29). */
+ * runs on the one-row GEMV (m = 1; 2-4 rows where out_dim <= 16 per CU, 2 rows
+ * also at larger out_dim when in_dim <= 4096), the multi-row decode kernel (up
+ * to 16 rows per launch, W8A8 32) and the MFMA GEMM (larger m).  IQ2_XS / IQ2_S /
+ * IQ3_S run on the one-row GEMV at m = 1 and on the multi-row decode kernel
+ * otherwise when the buffers are aligned (weight_bytes 16-byte or 8-byte,
+ * weight_scales 2-byte), and on a byte-load kernel for any other alignment.
+ * Bytes / scales per 256-weight block: 64/2, 64/10, 72/10, 104/6
+ * (src/iq2_matmul.rs:13-29). */
 typedef enum cmk_iq2_variant {
     CMK_IQ2_XXS = 0,
     CMK_IQ2_XS = 1,

@@ -1,8 +1,11 @@
 """The one-row GEMV's 2-4 row launch (iq2xxs_gemv.hip, kM4) against the fp64
 oracle.  The dispatch sends m = 2..4 there when out_dim <= 16 per CU (4096 on
-the 256 CUs of MI355X), the rows of x are 16-byte aligned, every digitisation
-task fits in registers at once (m * 32 * ceil(K/256) <= 2048) and the LDS
-holds m rows of digits; every shape below meets that.  Bars as in
+the 256 CUs of MI355X), and m = 2 also at larger out_dim when K <= 4096 (its
+packed two-operand form in mode Off), provided the rows of x are 16-byte
+aligned, every digitisation task fits in registers at once (m * 32 *
+ceil(K/256) <= 2048), one chunk of row groups per workgroup suffices and the
+LDS holds m rows of digits.  The shapes below reach it (14336 x 4096 at m = 2
+only; at m = 3, 4 it checks the multi-row kernel).  Bars as in
 test_gpu_parity.py (cond <= 1e-5, rel <= 1e-3 against the exact-weight fp64
 product; W8A8 against the reference's quantised activations), output classes
 exactly the oracle's for non-finite activations."""
@@ -17,7 +20,8 @@ torch = pytest.importorskip("torch")
 from test_gpu_edges import _check_classes_and_finite, classes  # noqa: E402
 from test_gpu_parity import errors, to_dev, x_as_f32, x_tensor  # noqa: E402
 
-SHAPES = [(4096, 4096), (1024, 4096), (4096, 2048), (37, 256), (300, 1000), (2048, 8192)]
+SHAPES = [(4096, 4096), (1024, 4096), (4096, 2048), (37, 256), (300, 1000), (2048, 8192),
+          (14336, 4096)]
 _DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
 
 
