@@ -1,8 +1,8 @@
 // iq2xxs_gemv.hip — decode-shaped IQ2_XXS matmul, one activation row, for
 // gfx950; also 2 to 4 rows where the multi-row kernel (iq2xxs_gemv_rows.hip,
-// which serves more rows) would leave CUs idle (out_dim <= 16 per CU): the
-// rows then take the places of the digit planes in the MFMA's A operand
-// (kM4, below).
+// which serves more rows) would leave CUs idle (out_dim <= 16 per CU), and 2
+// rows at any out_dim for K <= 4096: the rows then take the places of the
+// digit planes in the MFMA's A operand (kM4, below).
 //
 // Replaces iq2_xxs_matmul_kernel / iq2_xxs_matmul_w8a8_kernel
 // (src/metal_src/iq2_matmul.metal:188-240, 436-499), which run one thread per
@@ -843,8 +843,9 @@ __global__ __launch_bounds__(kGemvThreads) void iq2xxs_gemv_kernel(GemvArgs a) {
   // sum over the 16 blocks).  A row j is activation row j (rows past m read
   // zeros); per digit plane, from the highest, two chains of eight MFMAs, and
   // the planes combine as ((C2 * 256 + C1) * 256 + C0) in fp32 (two roundings
-  // of 2^-24 relative).  The digits are read per tile: the three planes of a
-  // row do not fit in registers next to the rest.
+  // of 2^-24 relative); two rows in mode Off pack their six (row, plane) pairs
+  // into two A operands instead.  The digits are read per tile: the three
+  // planes of a row do not fit in registers next to the rest.
   auto compute_tile4 = [&](uint32_t k) -> f32x4 {
     const uint32_t pair = min(tslice[k] * kSlicePairs + b, a.npairs - 1);
     const uint32_t nsb = a.bpr * 8;

@@ -70,10 +70,12 @@ def test_noalloc_matches_workspace_entry_point(pkg, inputs, dev, first, second):
         assert torch.equal(ref, got), (m, n, k, x_dtype, mode)
 
 
-def test_noalloc_gemv_needs_no_scratch(pkg, inputs, dev):
-    """The decode path needs no scratch: the same call on an m=1 shape."""
+@pytest.mark.parametrize("m", [1, 3])
+def test_noalloc_gemv_needs_no_scratch(pkg, inputs, dev, m):
+    """The decode paths need no scratch: the same call on the one-row GEMV
+    (m=1) and its 2-4 row launch (m=3)."""
     cabi = pkg.cabi
-    m, n, k = 1, 2048, 4096
+    n, k = 2048, 4096
     assert cabi.workspace_size(cabi.CMK_F32, m, n, k) == 0
     wb, ws = inputs.synthetic_weights(n, k)
     xt = torch.from_numpy(inputs.synthetic_x(m, k)).to(dev)
