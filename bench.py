@@ -650,6 +650,37 @@ def bench_mlp_step(pkg, torch, stream, steps, k=4096, n=14336):
             "gbs": step_bytes / (us * 1e-6) / 1e9, "steps": steps}
 
 
+def bench_tp8_shards(pkg, torch, stream, steps=300):
+    """One GPU's share of config 1 under 8-way tensor parallelism, at its real
+    shape (M=1, f32 x): gate and up split by output rows (K=4096, N=1792 each)
+    and down split by K (K=1792, N=4096, fp32 partials before the all-reduce).
+    Rotated weight copies, one HIP graph per shape, mean launch time.  The
+    collective itself is not measured (one GPU)."""
+    cabi, inputs = pkg.cabi, pkg.inputs
+    dev = torch.device("cuda:0")
+    sh = int(stream.cuda_stream)
+    res = {}
+    for name, k, n in (("gate_or_up_1_of_8", 4096, 1792), ("down_1_of_8", 1792, 4096)):
+        wb, ws = inputs.synthetic_weights(n, k)
+        copies = max(2, math.ceil(2 * MALL_BYTES / (wb.size + ws.size)))
+        wbt, wst = torch.from_numpy(wb).to(dev), torch.from_numpy(ws).to(dev)
+        reps = [(wbt, wst)] + [(wbt.clone(), wst.clone()) for _ in range(copies - 1)]
+        x = torch.from_numpy(inputs.synthetic_x(1, k)).to(dev)
+        out = torch.empty((1, n), dtype=torch.float32, device=dev)
+        calls = [Matmul(cabi, x, r[0], r[1], out, 1, k, n, cabi.CMK_F32, sh) for r in reps]
+        for c in calls:
+            c()
+        torch.cuda.synchronize()
+        us = _timed_graph(torch, cabi, stream, sh, lambda i: calls[i % copies](), steps)
+        b = alg_bytes(1, k, n)
+        res[name] = {"k": k, "n": n, "us_per_launch": us, "alg_bytes": b,
+                     "gbs": b / (us * 1e-6) / 1e9}
+        log(f"[bench] tp8 shard {name} (K={k} N={n}): {us:.2f} us per launch, "
+            f"{res[name]['gbs']:.1f} GB/s")
+        del reps, calls
+    return res
+
+
 def bench_gguf_split(pkg, torch, stream, steps, k=4096, n=14336):
     """GGUF (ggml) IQ2_XXS blocks of the gate matrix split into the reference's
     pair: bytes moved (read + written) per launch over its duration."""
@@ -849,6 +880,7 @@ def main():
         variants = (None if args.no_variants
                     else bench_variants(pkg, torch, stream, args.variant_steps))
         split = None if args.no_variants else bench_gguf_split(pkg, torch, stream, 50)
+        shards = None if args.no_variants else bench_tp8_shards(pkg, torch, stream)
         refw = None if args.no_variants else bench_reference_workload(pkg, torch, stream)
         mlp = None if args.no_variants else bench_mlp_step(pkg, torch, stream, 300)
         configs = None if args.no_configs else bench_configs(pkg, torch, stream)
@@ -889,6 +921,8 @@ def main():
         line["variants_m1"] = variants
     if split is not None:
         line["gguf_split"] = split
+    if shards is not None:
+        line["tp8_shard_m1"] = shards
     if refw is not None:
         line["reference_bench_workload"] = refw
     if mlp is not None:
