@@ -22,6 +22,10 @@ from test_gpu_parity import errors, to_dev, x_as_f32, x_tensor  # noqa: E402
 
 SHAPES = [(4096, 4096), (1024, 4096), (4096, 2048), (37, 256), (300, 1000), (2048, 8192),
           (14336, 4096)]
+
+
+def _fits(m, k):
+    return m * 32 * ((k + 255) // 256) <= 2048
 _DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
 
 
@@ -33,10 +37,6 @@ def dev(pkg):
     return torch.device("cuda:0")
 
 
-def _fits(m, k):
-    return m * 32 * ((k + 255) // 256) <= 2048
-
-
 def _run(pkg, xt, wb, ws, n, k, w8a8):
     mode = pkg.ActivationQuantMode.W8A8 if w8a8 else pkg.ActivationQuantMode.Off
     cfg = pkg.ActivationQuantConfig(mode, False)
@@ -44,13 +44,15 @@ def _run(pkg, xt, wb, ws, n, k, w8a8):
                                                 cfg).cpu().numpy()
 
 
+# (m, n, k): every shape at every m whose digitisation tasks fit the launch
+# (m * 32 * ceil(K/256) <= 2048; 2048 x 8192 only at m = 2)
+_MNK = [(m, n, k) for m in (2, 3, 4) for n, k in SHAPES if _fits(m, k)]
+
+
 @pytest.mark.parametrize("w8a8", [False, True], ids=["off", "w8a8"])
 @pytest.mark.parametrize("dtype", sorted(_DT))
-@pytest.mark.parametrize("n,k", SHAPES)
-@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("m,n,k", _MNK)
 def test_m4_vs_oracle(pkg, oracle, inputs, dev, m, n, k, dtype, w8a8):
-    if not _fits(m, k):
-        pytest.skip("takes the multi-row kernel (digitisation tasks beyond two rounds)")
     wb, ws = inputs.synthetic_weights(n, k, seed=m * 7 + n + k)
     xt = x_tensor(inputs.synthetic_x(m, k, seed=m + 1), _DT[dtype], dev)
     y = _run(pkg, xt, to_dev(wb, dev), to_dev(ws, dev), n, k, w8a8).reshape(m, n)
