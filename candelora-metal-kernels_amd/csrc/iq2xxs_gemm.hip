@@ -57,6 +57,7 @@
 // Bound: MFMA (arithmetic intensity ~1200 flop/B at m = 512).
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "iq2xxs_device.h"
 #include "iq2xxs_kernels.h"
@@ -263,19 +264,25 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
         T.sgn[gg] = gemm_lds_u4(kGemmSign + __builtin_amdgcn_ubfe(aux_s, 7 * g, 7) * (16 * kGemmSignCopies) + css);
       }
     };
-    auto write_w = [&](uint32_t t, uint32_t aux_s, uint32_t dbits, const Tables& T) {
-      // exact fp32 level values l * d * (2s + 1) / 8, then one rounding each
-      const float tdf = half_bits_to_float((uint16_t)dbits) * (float)((aux_s >> 27) | 1u) * 0.125f;
-      const uint32_t pool_lo = pack2(8.0f * tdf, 25.0f * tdf);
-      const uint32_t pool_hi = pack2(43.0f * tdf, 0.0f);
-#pragma unroll
-      for (int gg = 0; gg < 2; ++gg) {
-        const u32x4 v = {__builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].x) ^ T.sgn[gg].x,
-                         __builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].y) ^ T.sgn[gg].y,
-                         __builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].z) ^ T.sgn[gg].z,
-                         __builtin_amdgcn_perm(pool_hi, pool_lo, T.sel[gg].w) ^ T.sgn[gg].w};
-        gemm_lds_store((gg ? wdst1 : wdst0) + t * L::kBStage, v);
-      }
+    // The level values l * d * (2s + 1) / 8 of a sub-block, l in {8, 25, 43},
+    // each rounded once to f16 (exact in fp32 before the rounding): the
+    // conversion of s * 2^28 + 2^27 - 1 rounds to (2s + 1) * 2^27 exactly,
+    // and d * 2^-30 is exact.
+    struct Pool {
+      uint32_t lo, hi;
+    };
+    auto level_pool = [](uint32_t aux_s, uint32_t dbits) {
+      const float s27 = (float)((aux_s & 0xF0000000u) | 0x07FFFFFFu);
+      const float tdf = s27 * (half_bits_to_float((uint16_t)dbits) * 0x1p-30f);
+      return Pool{pack2(8.0f * tdf, 25.0f * tdf), pack2(43.0f * tdf, 0.0f)};
+    };
+    // group pair gg of weight tile t from the tables read one step earlier
+    auto store_group = [&](int gg, uint32_t t, const Pool& P, const Tables& T) {
+      const u32x4 v = {__builtin_amdgcn_perm(P.hi, P.lo, T.sel[gg].x) ^ T.sgn[gg].x,
+                       __builtin_amdgcn_perm(P.hi, P.lo, T.sel[gg].y) ^ T.sgn[gg].y,
+                       __builtin_amdgcn_perm(P.hi, P.lo, T.sel[gg].z) ^ T.sgn[gg].z,
+                       __builtin_amdgcn_perm(P.hi, P.lo, T.sel[gg].w) ^ T.sgn[gg].w};
+      gemm_lds_store((gg ? wdst1 : wdst0) + t * L::kBStage, v);
     };
     // codes of the stage at sub-block sb of its block, from set c
     auto aux_of = [](const Codes& c, int sb, uint32_t& aux_g, uint32_t& aux_s) {
@@ -289,32 +296,36 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
     // byte 16 l of the group, i.e. row (l >> 2), position l & 3, which holds
     // chunk (l & 3) ^ ((row >> 1) & 3) = (l & 3) ^ ((l >> 3) & 3).  A quad of
     // lanes reads one row's 64 contiguous bytes.  Rows past m and columns past
-    // in_dim read as zeros (out-of-range offsets).
+    // in_dim read as zeros: a row past m starts at kGemmOutOfRange, which
+    // stays out of range at every stage's offset, and a stage that reaches
+    // past in_dim checks each lane's chunk.
     const uint32_t pw = wave - 4;
     const __amdgpu_buffer_rsrc_t rx = gemm_rsrc(a.x, a.x_records);
     const uint32_t xkc = (lane & 3) ^ ((lane >> 3) & 3);
     // (fixed-size arrays: with arrays sized by L::kDma next to the DMA builtin,
     // hipcc's host pass silently emits no stub for the kernel)
     uint32_t xsrc[4];
-    bool xok[4];
     static_assert(L::kDma <= 4, "activation DMA per producer");
 #pragma unroll
     for (int k = 0; k < L::kDma; ++k) {
       const uint32_t row = 16 * (L::kDma * pw + k) + (lane >> 2);
-      xok[k] = m0 + row < a.m;
-      xsrc[k] = ((m0 + row) * a.in_dim + k0 + 8 * xkc) * 2;
+      xsrc[k] = m0 + row < a.m ? ((m0 + row) * a.in_dim + k0 + 8 * xkc) * 2 : kGemmOutOfRange;
     }
-    auto dma_x = [&](uint32_t s) {
-      const bool col_ok = k0 + kGemmBK * s + 8 * xkc < a.in_dim;
-      const uint32_t abuf = s & 3;
-#pragma unroll
-      for (int k = 0; k < L::kDma; ++k) {
-        const uint32_t dst = L::kA + abuf * L::kAStage + (L::kDma * pw + k) * 1024;
+    // Instruction k of stage s's DMA; `whole`: every column of the stage lies
+    // before in_dim (no per-lane check).
+    auto dma_one = [&](uint32_t s, int k, bool whole) {
+      if (k < L::kDma) {
+        const uint32_t dst = L::kA + (s & 3) * L::kAStage + (L::kDma * pw + k) * 1024;
+        const bool col_ok = whole || k0 + kGemmBK * s + 8 * xkc < a.in_dim;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rx, reinterpret_cast<__attribute__((address_space(3))) void*>(static_cast<uintptr_t>(dst)),
-            16, (xok[k] && col_ok) ? xsrc[k] + 64 * s : kGemmOutOfRange, 0, 0, 0);
+            16, col_ok ? xsrc[k] + 64 * s : kGemmOutOfRange, 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
+    };
+    auto dma_x = [&](uint32_t s) {
+#pragma unroll
+      for (int k = 0; k < L::kDma; ++k) dma_one(s, k, false);
     };
 
     Codes c0, c1;
@@ -333,34 +344,50 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
       read_tables(g0, s0v, t0);
       aux_of(c0, 1, g1, s1v);
       read_tables(g1, s1v, t1);
-      write_w(0, s0v, c0.d, t0);
+      const Pool P = level_pool(s0v, c0.d);
+      store_group(0, 0, P, t0);
+      store_group(1, 0, P, t0);
     }
     __syncthreads();  // stage 0 published (with its activations)
-    // Step s starts the DMA of the activations of stage s + 2 (their tile,
+    // Step s issues the DMA of the activations of stage s + 2 (their tile,
     // (s + 2) & 3, held stage s - 2, whose fragments were read before the
     // previous barrier), writes stage s (weight tile s & 1) from the tables
     // read one step earlier, then reads the tables of stage s + 1, and after
     // the last stage of a block reloads that code set with the block two
-    // ahead.  Its barrier publishes stage s: the weight writes must be done
-    // (the four table reads issued after them may stay in flight), and the
-    // DMA of stage s (issued two steps earlier) must have landed while the
-    // DMA of stages s + 1 and s + 2 and code loads may stay in flight.  A trip
-    // covers kGemmUnroll steps from s0 = 1 (mod 16), so every set choice and
-    // wait count below is a compile-time constant and the body is one
-    // straight-line sequence (exact wait counts).
-    for (uint32_t s0 = 1; s0 < nk_pad; s0 += kGemmUnroll) {
+    // ahead.  The DMA instructions are spread over the step (one before the
+    // level values, one before each group store, one after): a wave that
+    // issues them back to back waits for the memory pipeline to take each
+    // one, and its dequantisation waits with it.  Its barrier publishes
+    // stage s: the weight writes must be done (the four table reads issued
+    // after them may stay in flight), and the DMA of stage s (issued two
+    // steps earlier) must have landed while the DMA of stages s + 1 and
+    // s + 2 and code loads may stay in flight.  A trip covers kGemmUnroll
+    // steps from s0 = 1 (mod 16), so every set choice and wait count below is
+    // a compile-time constant and the body is one straight-line sequence
+    // (exact wait counts).  `whole`: the trip's DMA stages all end at or
+    // before in_dim.
+    auto trip = [&](uint32_t s0, auto whole_t) {
+      constexpr bool kWhole = decltype(whole_t)::value;
 #pragma unroll
       for (int j = 0; j < kGemmUnroll; ++j) {
         const uint32_t s = s0 + j;
         const int cj = 1 + j;  // s modulo 16
-        dma_x(s + 2);
         Codes& cc = ((cj >> 3) & 1) ? c1 : c0;        // block of stage s
         Codes& cn = (((cj + 1) >> 3) & 1) ? c1 : c0;  // block of stage s + 1
         Tables& tc = (cj & 1) ? t1 : t0;
         Tables& tn = (cj & 1) ? t0 : t1;
         uint32_t gn, sn, gc, sc;
         aux_of(cc, cj & 7, gc, sc);
-        write_w((uint32_t)(cj & 1), sc, cc.d, tc);
+        dma_one(s + 2, 0, kWhole);
+        const Pool P = level_pool(sc, cc.d);
+        __builtin_amdgcn_sched_barrier(0);
+        dma_one(s + 2, 1, kWhole);
+        store_group(0, (uint32_t)(cj & 1), P, tc);
+        __builtin_amdgcn_sched_barrier(0);
+        dma_one(s + 2, 2, kWhole);
+        store_group(1, (uint32_t)(cj & 1), P, tc);
+        __builtin_amdgcn_sched_barrier(0);
+        dma_one(s + 2, 3, kWhole);
         aux_of(cn, (cj + 1) & 7, gn, sn);
         read_tables(gn, sn, tn);
         if ((cj & 7) == 7) load_codes((s >> 3) + 2, cc);
@@ -373,6 +400,12 @@ __global__ __launch_bounds__(kGemmThreads) void iq2xxs_gemm_kernel(GemmArgs a) {
         else
           stage_barrier<2 * L::kDma, 4>();
       }
+    };
+    for (uint32_t s0 = 1; s0 < nk_pad; s0 += kGemmUnroll) {
+      if (k0 + kGemmBK * (s0 + kGemmUnroll + 2) <= a.in_dim)
+        trip(s0, std::true_type());
+      else
+        trip(s0, std::false_type());
     }
     return;
   }
