@@ -16,8 +16,8 @@
 //
 // Arithmetic.  The activations become exact integer digits as in the one-row
 // kernel (iq2xxs_gemv.hip): per 32-column sub-block, three signed 8-bit planes
-// of rint(x * 2^(D-e)), in LDS, with D = 22 bits for IQ2_XXS and 21 for the
-// other formats (the one-row kernel keeps 20 for IQ2_XXS).  The codes expand through the same
+// of rint(x * 2^(D-e)), in LDS, with D = 22 bits for IQ2_XXS (as in the
+// one-row kernel) and 21 for the other formats.  The codes expand through the same
 // LDS tables ({g, -g} codebook rows, 8-byte sign masks, one bit select per
 // dword).  v_mfma_i32_32x32x32_i8 then takes
 //   A: 32 rows = 8 activation rows x 4 digit planes (plane 3 and absent rows
