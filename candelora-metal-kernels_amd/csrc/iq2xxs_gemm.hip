@@ -20,7 +20,8 @@
 // Work split.  A workgroup computes a BM x BN tile of out; k advances in
 // stages of 32 columns (one 32-weight sub-block of every weight row).  For
 // m = 512, n = 14336 the tile is 256 x 112: 2 x 128 = 256 workgroups, one per
-// CU, and every weight sub-block is dequantised by two CUs only.
+// CU, and every weight sub-block is dequantised by two CUs only (256 x 128 or
+// 128 x 128 where those fill the CUs better; see plan_gemm).
 //  * Waves 0-3 (consumers) each own a 64 x BN/WN block of the tile.  They only
 //    read fragments from LDS and issue MFMAs: on gfx950 a wave's VALU work and
 //    memory-issue stalls do not overlap its own MFMAs, while work of another
@@ -57,6 +58,7 @@
 // Bound: MFMA (arithmetic intensity ~1200 flop/B at m = 512).
 #include <algorithm>
 #include <atomic>
+#include <cstdint>
 #include <type_traits>
 
 #include "iq2xxs_device.h"
@@ -802,29 +804,54 @@ __global__ __launch_bounds__(256) void gemm_split_reduce4_kernel(const float4* _
   }
 }
 
-// Tile shape and k split of one launch.  256 x 112 tiles halve the
+// Tile shape and k split of one launch.  256-row tiles halve the
 // dequantisation per CU and are used, above 128 rows, when they still give
 // most CUs a tile, and for 129-256 rows (one row block, where 128-row tiles
 // would decode every weight twice).  Up to 128 rows one 128-row block holds
 // them all: 256-row tiles would run half their MFMAs on padding rows (config
 // 4's gate / up at M = 128, f16 x: 97 us on 256 x 112 tiles).  When the tiles
 // cannot fill half of the 256 CUs, k is split (at least two blocks per split)
-// until they do.
+// until they do.  The 256-row tiles are 112 or 128 columns wide, whichever
+// leaves the busiest CU less work (rounds of 256 workgroups x columns x
+// blocks per split): 112 fills the CUs at N = 14336 and 28672 (128 or 256
+// tiles), 128 at N = 8192 (64 tiles, split four ways, where 112 gives 74
+// tiles split three ways: 222 workgroups).
 struct GemmPlan {
-  bool wide;  // 256 x 112 tiles (else 128 x 128)
+  bool wide;    // 256-row tiles (else 128 x 128)
+  uint32_t bn;  // columns of a 256-row tile: 112 or 128
   uint32_t splits, split_blocks;
 };
 
 static GemmPlan plan_gemm(uint32_t rows, uint32_t out_dim, uint32_t in_dim) {
   GemmPlan p;
   const uint32_t bpr = (in_dim + kQK - 1) / kQK;
-  const uint64_t t256 = (uint64_t)((rows + 255) / 256) * ((out_dim + 111) / 112);
+  const uint64_t row_tiles = (rows + 255) / 256;
+  const uint64_t t256 = row_tiles * ((out_dim + 111) / 112);
   p.wide = rows > 128 && (t256 >= 192 || rows <= 256);
-  const uint64_t tiles = p.wide ? t256 : (uint64_t)((rows + 127) / 128) * ((out_dim + 127) / 128);
-  uint64_t splits = 1;
-  if (tiles <= 128 && bpr >= 4) splits = std::min<uint64_t>(256 / tiles, bpr / 2);
-  p.split_blocks = (uint32_t)((bpr + splits - 1) / splits);
-  p.splits = (bpr + p.split_blocks - 1) / p.split_blocks;
+  auto split_of = [&](uint64_t tiles, uint32_t& splits, uint32_t& split_blocks) {
+    uint64_t sp = 1;
+    if (tiles <= 128 && bpr >= 4) sp = std::min<uint64_t>(256 / tiles, bpr / 2);
+    split_blocks = (uint32_t)((bpr + sp - 1) / sp);
+    splits = (bpr + split_blocks - 1) / split_blocks;
+  };
+  if (!p.wide) {
+    p.bn = 128;
+    split_of((uint64_t)((rows + 127) / 128) * ((out_dim + 127) / 128), p.splits, p.split_blocks);
+    return p;
+  }
+  uint64_t best = UINT64_MAX;
+  for (const uint32_t bn : {112u, 128u}) {
+    const uint64_t tiles = row_tiles * ((out_dim + bn - 1) / bn);
+    uint32_t sp, sb;
+    split_of(tiles, sp, sb);
+    const uint64_t cost = (tiles * sp + 255) / 256 * bn * sb;
+    if (cost < best) {  // (ties keep 112)
+      best = cost;
+      p.bn = bn;
+      p.splits = sp;
+      p.split_blocks = sb;
+    }
+  }
   return p;
 }
 
@@ -868,8 +895,9 @@ static hipError_t launch_gemm_shape(GemmArgs a, uint32_t out_rows, float* partia
     a.out = partials;
     a.out_split = n;
   }
-  const hipError_t e = p.wide ? launch_gemm_t<256, 112, kQ>(a, p.splits, stream)
-                              : launch_gemm_t<128, 128, kQ>(a, p.splits, stream);
+  const hipError_t e = !p.wide       ? launch_gemm_t<128, 128, kQ>(a, p.splits, stream)
+                       : p.bn == 128 ? launch_gemm_t<256, 128, kQ>(a, p.splits, stream)
+                                     : launch_gemm_t<256, 112, kQ>(a, p.splits, stream);
   if (e != hipSuccess || p.splits == 1) return e;
   if (n % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
       reinterpret_cast<uintptr_t>(partials) % 16 == 0) {

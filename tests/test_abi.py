@@ -164,9 +164,15 @@ def test_workspace_and_path_queries(cabi):
     assert cabi.matmul_path(cabi.CMK_F32, 17, 14336, 4096) == "gemm"
     assert cabi.workspace_size(cabi.CMK_F32, 16, 14336, 4096) == 0
     # (+ the k-split partials where the tiles cannot fill half of the 256 CUs:
-    # 256 staged rows x 8192 -> 74 tiles of 256 x 112, k split in 3 (11 blocks each))
+    # 256 staged rows x 8192 -> 64 tiles of 256 x 128, k split in 4 (8 blocks each):
+    # 256 x 112 tiles would be 74 split in 3 (11 blocks each, 222 workgroups))
     assert (cabi.workspace_size(cabi.CMK_F32, 128, 8192, 8192)
-            == 512 + 2 * 128 * 8192 * 2 + 3 * 128 * 8192 * 4)
+            == 512 + 2 * 128 * 8192 * 2 + 4 * 128 * 8192 * 4)
+    # N = 28672 keeps 256 x 112 (256 tiles, no split); N = 1024 too (10 tiles
+    # split in 16, where 256 x 128 gives 8 tiles split in 16)
+    assert cabi.workspace_size(cabi.CMK_F32, 128, 28672, 8192) == 512 + 2 * 128 * 8192 * 2
+    assert (cabi.workspace_size(cabi.CMK_F32, 128, 1024, 8192)
+            == 512 + 2 * 128 * 8192 * 2 + 16 * 128 * 1024 * 4)
     # 64 rows x 4096 -> 32 tiles, 16 blocks per row split in 8 (two blocks each)
     assert (cabi.workspace_size(cabi.CMK_F32, 64, 4096, 4096, mode=cabi.CMK_ACT_QUANT_W8A8)
             == 256 + 64 * 4096 * 2 + 8 * 64 * 4096 * 4)

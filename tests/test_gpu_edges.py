@@ -296,3 +296,42 @@ def test_config4_m128_vs_device_dequant(pkg, inputs, dev, dtype, out_dim, in_dim
     # error is the fp32 accumulation's; f16 x is exact in the MFMA.
     assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
     del w, x64, y64, sc
+
+
+# Shapes whose plan takes 256 x 128 tiles (the GEMM rows 129-256 and N near
+# 8192, where 112-column tiles leave CUs idle): ragged N, K not a multiple of
+# 256 or of a 32-column stage, a partial row tile, f32 rows staged as head /
+# tail pairs (m = 100: 200 GEMM rows), bf16 rows staged as scaled f16, W8A8.
+TILES_256x128 = [(200, 8000, 4096, torch.float16, False), (150, 8000, 3000, torch.bfloat16, False),
+                 (100, 8192, 4104, torch.float32, False), (130, 8100, 2560, torch.float16, True)]
+
+
+@pytest.mark.parametrize("m,out_dim,in_dim,dtype,w8a8", TILES_256x128)
+def test_gemm_256x128_tiles(pkg, oracle, inputs, dev, m, out_dim, in_dim, dtype, w8a8):
+    """The 256 x 128 tiles against an fp64 product with the device
+    dequantisation to f16 (W8A8: of the reference's quantised rows), at the
+    bars of the other GEMM shapes."""
+    wb, ws = inputs.synthetic_weights(out_dim, in_dim, seed=m)
+    wbt, wst = to_dev(wb, dev), to_dev(ws, dev)
+    xt = x_tensor(inputs.synthetic_x(m, in_dim, seed=m + 1), dtype, dev)
+    assert pkg.cabi.matmul_path(pkg.cabi.CMK_F32, m, out_dim, in_dim) == "gemm"
+    w = pkg.iq2_dequantize_to_f16(wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs,
+                                  out_dtype=torch.float16).double()
+    if w8a8:
+        cfg = pkg.ActivationQuantConfig(pkg.ActivationQuantMode.W8A8, False)
+        y = pkg.iq2_matmul_with_activation_quant(xt, wbt, wst, out_dim, in_dim,
+                                                 pkg.Iq2MatmulVariant.Iq2Xxs, cfg).double()
+        x64 = torch.from_numpy(
+            oracle.rowwise_qdq_w8a8(x_as_f32(xt), m, in_dim).astype(np.float64)).to(dev)
+    else:
+        y = pkg.iq2_matmul(xt, wbt, wst, out_dim, in_dim, pkg.Iq2MatmulVariant.Iq2Xxs).double()
+        x64 = xt.double()
+    y64 = x64 @ w.T
+    sc = x64.abs() @ w.abs().T
+    cond, rel = errors(y.cpu().numpy(), y64.cpu().numpy(), sc.cpu().numpy())
+    # W8A8 divides the fp32 sums of q * w by inv where the reference rounds
+    # q / inv first: the bars of test_gpu_parity's W8A8 GEMM test.
+    if w8a8:
+        assert cond <= 1e-4 and rel <= 1e-2, (cond, rel)
+    else:
+        assert cond <= 1e-5 and rel <= 1e-3, (cond, rel)
