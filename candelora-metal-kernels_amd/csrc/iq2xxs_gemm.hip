@@ -59,6 +59,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdint>
+#include <initializer_list>
 #include <type_traits>
 
 #include "iq2xxs_device.h"
